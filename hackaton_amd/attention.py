@@ -1,0 +1,413 @@
+"""Packed (padding-free) varlen causal GQA attention on MI355X: the reference's autograd surface
+(solution/attention.py) over hand-written gfx950 HIP kernels reached through the C ABI.
+
+Public surface, same names, argument order and number of returned gradients as the reference:
+
+    qkv_rotate(q, k, v, cos, sin, b_idx, t_idx, batch, seq, heads, kv_heads, padded=False)
+                                    solution/attention.py:191 (QKVRotate 150-188)
+    varlen_attention(query, key, value, lengths, scale)
+                                    solution/attention.py:236-242 (VarlenAttention 212-233)
+    packed_attention(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale)
+                                    solution/attention.py:282-285 (PackedAttention 250-279)
+    pack_rows(attn, b_idx, t_idx)   solution/attention.py:328 (PackRows 303-325)
+
+Differences that keep the drop-in contract:
+* `varlen_attention` accepts key/value with Hkv heads (GQA-native: the kernels read each key/value
+  head once for its G query heads) as well as the reference's expanded Hq-head form.
+* `packed_attention` rotates q and k without expanding K/V to the query heads and runs the
+  attention on Hkv key/value heads; the backward sums dK/dV over each GQA group inside the
+  attention kernel (fp32) and applies the inverse rotation straight from the fp32 accumulators.
+* fp16 and bf16 inputs both run on the MFMA kernels (the reference computes in fp16 only).
+
+Every op requires the HIP library and CUDA (HIP) tensors; there is no other implementation.
+"""
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check, lib
+from .offload import OFFLOADER
+
+HEAD_DIM = 128
+
+_DTYPES = {torch.float16: _lib.VA_F16, torch.bfloat16: _lib.VA_BF16, torch.float32: _lib.VA_F32}
+
+
+def _stream():
+    return ctypes_stream(torch.cuda.current_stream())
+
+
+def ctypes_stream(stream):
+    return stream.cuda_stream
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("hackaton_amd attention runs on the GPU only: got a tensor on "
+                             f"{t.device}")
+
+
+def _attn_dtype(t):
+    if t.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"attention inputs must be float16 or bfloat16, got {t.dtype}")
+    return _DTYPES[t.dtype]
+
+
+# ------------------------------------------------------------------------------------------------
+# cu_seqlens and work plans
+# ------------------------------------------------------------------------------------------------
+_CU_SEQLENS = {}
+_PLANS = {}
+
+
+def _cu_seqlens(lengths, device):
+    """int32 [0, l0, l0 + l1, ...] on the device, built once per batch shape (the 28 layers share
+    it), as solution/attention.py:198-209. The lengths ride along on the tensor so the work plan
+    is built on the host without reading the device."""
+    key = (device, tuple(lengths))
+    cu = _CU_SEQLENS.get(key)
+    if cu is None:
+        if len(_CU_SEQLENS) > 16:
+            _CU_SEQLENS.clear()
+        offsets = [0]
+        for length in lengths:
+            offsets.append(offsets[-1] + int(length))
+        cu = torch.tensor(offsets, dtype=torch.int32, device=device)
+        cu._va_offsets = tuple(offsets)
+        _CU_SEQLENS[key] = cu
+    return cu
+
+
+class Plan:
+    """Device work lists of the forward and backward kernels for one (cu_seqlens, Hq, Hkv)."""
+
+    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "offsets")
+
+    def __init__(self, offsets, hq, hkv, device):
+        cu = np.ascontiguousarray(np.asarray(offsets, dtype=np.int32))
+        self.offsets = tuple(int(x) for x in cu)
+        self.total = int(cu[-1])
+        items = []
+        for kind in (_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD):
+            items.append(build_plan_host(cu, hq, hkv, kind))
+        host_fwd, host_bwd = items
+        self.n_fwd, self.n_bwd = host_fwd.shape[0], host_bwd.shape[0]
+        self.fwd_items = torch.from_numpy(host_fwd).to(device)
+        self.bwd_items = torch.from_numpy(host_bwd).to(device)
+
+
+def build_plan_host(cu, hq, hkv, kind):
+    """Work items (n, 4) int32 from the C planner (host only)."""
+    cu = np.ascontiguousarray(np.asarray(cu, dtype=np.int32))
+    n_docs = cu.shape[0] - 1
+    n = np.zeros(1, dtype=np.int64)
+    cu_p = cu.ctypes.data_as(_lib._pi32)
+    check(lib().va_plan_size(cu_p, n_docs, hq, hkv, kind, n.ctypes.data_as(_lib._pi64)),
+          "va_plan_size")
+    items = np.zeros((max(int(n[0]), 1), 4), dtype=np.int32)
+    written = np.zeros(1, dtype=np.int64)
+    check(lib().va_plan_build(cu_p, n_docs, hq, hkv, kind, items.ctypes.data_as(_lib._pi32),
+                              int(n[0]), written.ctypes.data_as(_lib._pi64)), "va_plan_build")
+    return items[: int(n[0])]
+
+
+def _plan(cu_seqlens, hq, hkv):
+    offsets = getattr(cu_seqlens, "_va_offsets", None)
+    if offsets is None:  # a cu_seqlens tensor not made by _cu_seqlens: read it (one sync)
+        offsets = tuple(int(x) for x in cu_seqlens.cpu().tolist())
+    key = (cu_seqlens.device, offsets, hq, hkv)
+    plan = _PLANS.get(key)
+    if plan is None:
+        if len(_PLANS) > 32:
+            _PLANS.clear()
+        plan = _PLANS[key] = Plan(offsets, hq, hkv, cu_seqlens.device)
+    return plan
+
+
+# ------------------------------------------------------------------------------------------------
+# attention forward / backward through the C ABI
+# ------------------------------------------------------------------------------------------------
+def attention_forward(query, key, value, plan, scale):
+    """(out (N, Hq, D), lse (Hq, N) fp32) of packed causal attention; query (N, Hq, D),
+    key/value (N, Hkv, D), all contiguous, same 16-bit dtype."""
+    _require_device(query, key, value)
+    dtype = _attn_dtype(query)
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise ValueError("query, key and value must share a dtype")
+    n, hq, d = query.shape
+    hkv = key.shape[1]
+    if key.shape != (n, hkv, d) or value.shape != key.shape:
+        raise ValueError(f"shape mismatch: q {tuple(query.shape)} k {tuple(key.shape)} "
+                         f"v {tuple(value.shape)}")
+    if n != plan.total:
+        raise ValueError(f"{n} tokens but cu_seqlens covers {plan.total}")
+    out = torch.empty_like(query)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=query.device)
+    check(lib().va_fwd(_ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
+                       _ptr(plan.fwd_items), plan.n_fwd, n, hq, hkv, d, float(scale), dtype,
+                       _stream()), "va_fwd")
+    return out, lse
+
+
+def bwd_workspace(n, hq, hkv, device):
+    offsets = np.zeros(4, dtype=np.int64)
+    nbytes = np.zeros(1, dtype=np.int64)
+    check(lib().va_bwd_workspace_layout(n, hq, hkv, HEAD_DIM, offsets.ctypes.data_as(_lib._pi64),
+                                        nbytes.ctypes.data_as(_lib._pi64)),
+          "va_bwd_workspace_layout")
+    return torch.empty(int(nbytes[0]), dtype=torch.uint8, device=device), [int(x) for x in offsets]
+
+
+def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=True):
+    """dq, dk, dv (dk/dv summed over each GQA group). With outputs=False returns the fp32
+    accumulators (N, Hq, D), (N, Hkv, D), (N, Hkv, D) that live in the workspace."""
+    n, hq, d = query.shape
+    hkv = key.shape[1]
+    dtype = _attn_dtype(query)
+    grad = grad.reshape(out.shape)
+    if grad.dtype != query.dtype:
+        grad = grad.to(query.dtype)
+    grad = grad.contiguous()
+    ws, offs = bwd_workspace(n, hq, hkv, query.device)
+    if outputs:
+        dq, dk, dv = torch.empty_like(query), torch.empty_like(key), torch.empty_like(value)
+    else:
+        dq = dk = dv = None
+    check(lib().va_bwd(_ptr(grad), _ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
+                       _ptr(plan.bwd_items), plan.n_bwd, n, hq, hkv, d, float(scale), dtype,
+                       _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(), _stream()), "va_bwd")
+    if outputs:
+        return dq, dk, dv
+
+    def view(off, shape):
+        count = int(np.prod(shape))
+        return ws[off: off + 4 * count].view(torch.float32).view(*shape)
+
+    return view(offs[1], (n, hq, d)), view(offs[2], (n, hkv, d)), view(offs[3], (n, hkv, d)), ws
+
+
+class VarlenAttention(torch.autograd.Function):
+    """Causal attention of every document of the packed rows in one launch of the gfx950 forward
+    kernel (and three of the backward), given the document boundaries `cu_seqlens`.
+    Inputs (N, H, D) query and (N, Hkv, D) key/value (Hkv = H, the reference's expanded form, or
+    the GQA kv heads), output (N, H * D). solution/attention.py:212-233."""
+
+    @staticmethod
+    def forward(ctx, query, key, value, cu_seqlens, max_len, scale):
+        plan = _plan(cu_seqlens, query.shape[1], key.shape[1])
+        out, lse = attention_forward(query, key, value, plan, scale)
+        ctx.save_for_backward(query, key, value, out, lse, cu_seqlens)
+        ctx.max_len, ctx.scale, ctx.plan = max_len, scale, plan
+        return out.reshape(query.shape[0], -1)
+
+    @staticmethod
+    def backward(ctx, grad):
+        query, key, value, out, lse, _cu = ctx.saved_tensors
+        dq, dk, dv = attention_backward(grad, query, key, value, out, lse, ctx.plan, ctx.scale)
+        return dq, dk, dv, None, None, None
+
+
+def varlen_attention(query, key, value, lengths, scale):
+    """Causal attention of each sequence on its own, on packed (N, H, D) rows where sequence i is
+    the contiguous block of `lengths[i]` rows; returns (N, H * D). solution/attention.py:236-242."""
+    lengths = [int(length) for length in lengths if int(length) > 0]
+    cu_seqlens = _cu_seqlens(lengths, query.device)
+    return VarlenAttention.apply(query.contiguous(), key.contiguous(), value.contiguous(),
+                                 cu_seqlens, max(lengths), scale)
+
+
+# ------------------------------------------------------------------------------------------------
+# rotary embedding
+# ------------------------------------------------------------------------------------------------
+def _rope_strides(cos):
+    scb = 0 if cos.shape[0] == 1 else cos.stride(0)
+    return scb, cos.stride(1)
+
+
+def _tables(cos, sin):
+    cos = cos.float().contiguous()
+    sin = sin.float().contiguous()
+    if cos.shape != sin.shape or cos.dim() != 3 or cos.shape[-1] != HEAD_DIM:
+        raise ValueError(f"cos/sin must be (1 or B, T, {HEAD_DIM}), got {tuple(cos.shape)}")
+    return cos, sin
+
+
+def rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads, out_dtype, layout=0,
+                 expand=False, batch=0, seq=0):
+    """Rotated q, k and cast v as three tensors of `out_dtype`, in the packed (N, H, D) or the
+    zero-filled padded (B, H, T, D) layout; K/V keep kv_heads unless `expand`."""
+    _require_device(q, k, v, cos, sin, b_idx, t_idx)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    cos, sin = _tables(cos, sin)
+    n = q.shape[0]
+    kvo = heads if expand else kv_heads
+    if layout == _lib.VA_LAYOUT_PADDED:
+        qo = torch.zeros(batch, heads, seq, HEAD_DIM, dtype=out_dtype, device=q.device)
+        ko, vo = torch.zeros_like(qo), torch.zeros_like(qo)
+    else:
+        qo = torch.empty(n, heads, HEAD_DIM, dtype=out_dtype, device=q.device)
+        ko = torch.empty(n, kvo, HEAD_DIM, dtype=out_dtype, device=q.device)
+        vo = torch.empty_like(ko)
+    if q.shape[1] != heads * HEAD_DIM or k.shape[1] != kv_heads * HEAD_DIM or v.shape != k.shape:
+        raise ValueError("projection shapes do not match heads * head_dim")
+    scb, sct = _rope_strides(cos)
+    check(lib().va_rope_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), scb, sct,
+                            _ptr(b_idx), _ptr(t_idx), _ptr(qo), _ptr(ko), _ptr(vo), n, heads,
+                            kv_heads, HEAD_DIM, seq, _DTYPES[q.dtype], _DTYPES[out_dtype], layout,
+                            int(expand), _stream()), "va_rope_fwd")
+    return qo, ko, vo
+
+
+def rope_backward(dq, dk, dv, cos, sin, b_idx, t_idx, heads, kv_heads, out_dtype, layout=0,
+                  expand=False, seq=0):
+    """Projection gradients (N, heads*D), (N, kv_heads*D) x2 in `out_dtype` from the gradients of
+    the rotated tensors (expanded ones are summed over each GQA group first)."""
+    n = b_idx.shape[0]
+    dq, dk, dv = dq.contiguous(), dk.contiguous(), dv.contiguous()
+    cos, sin = _tables(cos, sin)
+    dq_in = torch.empty(n, heads * HEAD_DIM, dtype=out_dtype, device=dq.device)
+    dk_in = torch.empty(n, kv_heads * HEAD_DIM, dtype=out_dtype, device=dq.device)
+    dv_in = torch.empty_like(dk_in)
+    scb, sct = _rope_strides(cos)
+    if not (dq.dtype == dk.dtype == dv.dtype):
+        raise ValueError("gradient dtypes differ")
+    check(lib().va_rope_bwd(_ptr(dq), _ptr(dk), _ptr(dv), _ptr(cos), _ptr(sin), scb, sct,
+                            _ptr(b_idx), _ptr(t_idx), _ptr(dq_in), _ptr(dk_in), _ptr(dv_in), n,
+                            heads, kv_heads, HEAD_DIM, seq, _DTYPES[dq.dtype], _DTYPES[out_dtype],
+                            layout, int(expand), _stream()), "va_rope_bwd")
+    return dq_in, dk_in, dv_in
+
+
+class QKVRotate(torch.autograd.Function):
+    """Packed (q, k, v) projections (N, heads * D) -> rotated, fp16, GQA-expanded heads:
+    (N, H, D) each when `padded` is False, (B, H, T, D) each when it is True.
+    solution/attention.py:150-188 (same outputs and the same 12 returned gradients)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin, b_idx, t_idx, batch, seq, heads, kv_heads, padded):
+        layout = _lib.VA_LAYOUT_PADDED if padded else _lib.VA_LAYOUT_PACKED
+        qo, ko, vo = rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads,
+                                  torch.float16, layout, True, batch, seq)
+        ctx.save_for_backward(cos, sin, b_idx, t_idx)
+        ctx.meta = (seq, heads, kv_heads, q.dtype, layout)
+        return qo, ko, vo
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        cos, sin, b_idx, t_idx = ctx.saved_tensors
+        seq, heads, kv_heads, dtype, layout = ctx.meta
+        dq_in, dk_in, dv_in = rope_backward(dq.half(), dk.half(), dv.half(), cos, sin, b_idx,
+                                            t_idx, heads, kv_heads, dtype, layout, True, seq)
+        return dq_in, dk_in, dv_in, None, None, None, None, None, None, None, None, None
+
+
+def qkv_rotate(q, k, v, cos, sin, b_idx, t_idx, batch, seq, heads, kv_heads, padded=False):
+    return QKVRotate.apply(q, k, v, cos, sin, b_idx, t_idx, batch, seq, heads, kv_heads, padded)
+
+
+# ------------------------------------------------------------------------------------------------
+# rotation + attention of the packed rows (the decoder layer's call)
+# ------------------------------------------------------------------------------------------------
+def _compute_dtype(proj_dtype):
+    """Element type the attention runs in: bf16 projections stay bf16, everything else runs in
+    fp16 like the reference (solution/attention.py:21-22: one rounding to fp16 after the rotation)."""
+    return torch.bfloat16 if proj_dtype == torch.bfloat16 else torch.float16
+
+
+def _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale):
+    """Rotation (no K/V expansion) + varlen attention; returns (out (N,Hq,D), lse, rotated q/k/v,
+    plan). solution/attention.py:245-247."""
+    lengths = [int(length) for length in lengths if int(length) > 0]
+    cu = _cu_seqlens(lengths, q.device)
+    plan = _plan(cu, heads, kv_heads)
+    qr, kr, vr = rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads,
+                              _compute_dtype(q.dtype))
+    out, lse = attention_forward(qr, kr, vr, plan, scale)
+    return out, lse, (qr, kr, vr), plan
+
+
+class PackedAttention(torch.autograd.Function):
+    """Rotation + per-sequence causal attention of the packed rows, (N, heads * D) out.
+
+    Keeps only the three projections for the backward (in pinned host memory when `offload`) and
+    recomputes the rotation and the attention forward in the backward, like
+    solution/attention.py:250-279; the backward then runs the attention backward kernels (dK/dV
+    summed over each GQA group in fp32) and the inverse rotation straight from the fp32
+    accumulators. Returns the three projection gradients and 10 Nones."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale,
+                offload):
+        with torch.no_grad():
+            out, _lse, _rot, _plan_ = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
+                                              kv_heads, lengths, scale)
+        ctx.consts = (cos, sin, b_idx, t_idx)
+        ctx.meta = (seq, heads, kv_heads, lengths, scale)
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype)
+        if offload:
+            ctx.item = OFFLOADER.save(q, k, v)
+        else:
+            ctx.save_for_backward(q, k, v)
+        return out.reshape(q.shape[0], -1).to(_compute_dtype(q.dtype))
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v = OFFLOADER.load(ctx.item) if hasattr(ctx, "item") else ctx.saved_tensors
+        cos, sin, b_idx, t_idx = ctx.consts
+        seq, heads, kv_heads, lengths, scale = ctx.meta
+        out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
+                                               kv_heads, lengths, scale)
+        dq_acc, dk_acc, dv_acc, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
+                                                         outputs=False)
+        dq, dk, dv = rope_backward(dq_acc, dk_acc, dv_acc, cos, sin, b_idx, t_idx, heads,
+                                   kv_heads, q.dtype)
+        grads = (dq, dk.to(k.dtype), dv.to(v.dtype))
+        return (*grads, None, None, None, None, None, None, None, None, None, None)
+
+
+def packed_attention(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale):
+    offload = OFFLOADER.wants(q, k, v) and (q.requires_grad or k.requires_grad or v.requires_grad)
+    return PackedAttention.apply(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths,
+                                 scale, offload)
+
+
+# ------------------------------------------------------------------------------------------------
+# padded -> packed rows (fallback layout)
+# ------------------------------------------------------------------------------------------------
+class PackRows(torch.autograd.Function):
+    """(B, H, T, D) attention output -> (N, H * D) rows of the real tokens (fallback path).
+    solution/attention.py:303-325."""
+
+    @staticmethod
+    def forward(ctx, attn, b_idx, t_idx):
+        _require_device(attn, b_idx, t_idx)
+        batch, heads, seq, dim = attn.shape
+        attn = attn.contiguous()
+        out = torch.empty(b_idx.shape[0], heads * dim, dtype=attn.dtype, device=attn.device)
+        check(lib().va_pack_rows(_ptr(attn), _ptr(out), _ptr(b_idx), _ptr(t_idx), b_idx.shape[0],
+                                 heads, seq, dim, attn.element_size(), 0, _stream()),
+              "va_pack_rows")
+        ctx.save_for_backward(b_idx, t_idx)
+        ctx.meta = (batch, heads, seq, dim)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        b_idx, t_idx = ctx.saved_tensors
+        batch, heads, seq, dim = ctx.meta
+        grad = grad.contiguous()
+        padded = torch.zeros(batch, heads, seq, dim, dtype=grad.dtype, device=grad.device)
+        check(lib().va_pack_rows(_ptr(grad), _ptr(padded), _ptr(b_idx), _ptr(t_idx),
+                                 b_idx.shape[0], heads, seq, dim, grad.element_size(), 1,
+                                 _stream()), "va_pack_rows")
+        return padded, None, None
+
+
+def pack_rows(attn, b_idx, t_idx):
+    return PackRows.apply(attn, b_idx, t_idx)

@@ -1,0 +1,104 @@
+// Host-side work planning for the varlen attention kernels (no GPU calls).
+//
+// The plan turns cu_seqlens into a list of work items, one per (tile, query head): tiles never
+// cross a document boundary and never start past the causal diagonal, so fully masked causal
+// tiles and cross-document tiles are never launched. Items are ordered by decreasing work
+// (longest-processing-time first): the hardware dispatcher hands work-groups out in index order,
+// so the longest tiles start first and the short ones fill the tail.
+#include <algorithm>
+#include <cstdint>
+#include <vector>
+
+#include "../../include/varlen_attn.h"
+#include "va_api_internal.h"
+#include "va_kernels.h"
+
+namespace {
+
+struct Item {
+  int32_t a, b, c, d;
+  int64_t work;
+};
+
+int check_cu(const int32_t* cu, int32_t n_docs) {
+  if (n_docs < 0) return va::fail(VA_EINVAL, "n_docs < 0");
+  if (cu == nullptr) return va::fail(VA_EINVAL, "cu_seqlens is NULL");
+  if (cu[0] != 0) return va::fail(VA_ESEQ, "cu_seqlens[0] != 0");
+  for (int32_t i = 0; i < n_docs; ++i) {
+    if (cu[i + 1] < cu[i]) return va::fail(VA_ESEQ, "cu_seqlens decreases at %d", i);
+  }
+  return VA_OK;
+}
+
+int check_heads(int32_t hq, int32_t hkv) {
+  if (hq <= 0 || hkv <= 0) return va::fail(VA_ESHAPE, "heads must be positive (%d, %d)", hq, hkv);
+  if (hq % hkv != 0) return va::fail(VA_ESHAPE, "Hq=%d is not a multiple of Hkv=%d", hq, hkv);
+  if (hq > 4096) return va::fail(VA_ESHAPE, "Hq=%d out of range", hq);
+  return VA_OK;
+}
+
+std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
+  std::vector<Item> items;
+  for (int32_t i = 0; i < n_docs; ++i) {
+    const int32_t s = cu[i], e = cu[i + 1];
+    if (e <= s) continue;
+    if (kind == VA_PLAN_FWD) {
+      for (int32_t q0 = s; q0 < e; q0 += va::kFwdBlockM) {
+        const int32_t kv_end = std::min<int64_t>((int64_t)q0 + va::kFwdBlockM, e);
+        const int64_t work = kv_end - s;  // keys visited by the tile
+        for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, h, work});
+      }
+    } else {
+      for (int32_t k0 = s; k0 < e; k0 += va::kBwdBlockN) {
+        const int64_t work = e - k0;  // queries visited by the tile
+        for (int32_t h = 0; h < hq; ++h) items.push_back({k0, e, h, 1, work});
+      }
+    }
+  }
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item& x, const Item& y) { return x.work > y.work; });
+  return items;
+}
+
+int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
+  int64_t n = 0;
+  const int64_t tile = kind == VA_PLAN_FWD ? va::kFwdBlockM : va::kBwdBlockN;
+  for (int32_t i = 0; i < n_docs; ++i) {
+    const int64_t len = (int64_t)cu[i + 1] - cu[i];
+    if (len > 0) n += (len + tile - 1) / tile * hq;
+  }
+  return n;
+}
+
+}  // namespace
+
+extern "C" int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv,
+                            int32_t kind, int64_t* n_items) {
+  if (n_items == nullptr) return va::fail(VA_EINVAL, "n_items is NULL");
+  if (kind != VA_PLAN_FWD && kind != VA_PLAN_BWD) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
+  int rc = check_heads(hq, hkv);
+  if (rc) return rc;
+  rc = check_cu(cu_seqlens, n_docs);
+  if (rc) return rc;
+  *n_items = count_items(cu_seqlens, n_docs, hq, kind);
+  return VA_OK;
+}
+
+extern "C" int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv,
+                             int32_t kind, int32_t* items, int64_t capacity, int64_t* n_items) {
+  int64_t n = 0;
+  int rc = va_plan_size(cu_seqlens, n_docs, hq, hkv, kind, &n);
+  if (rc) return rc;
+  if (n_items) *n_items = n;
+  if (n > capacity) return va::fail(VA_ECAPACITY, "plan needs %lld items, capacity %lld",
+                                    (long long)n, (long long)capacity);
+  if (n > 0 && items == nullptr) return va::fail(VA_EINVAL, "items is NULL");
+  const std::vector<Item> v = make_items(cu_seqlens, n_docs, hq, kind);
+  for (size_t i = 0; i < v.size(); ++i) {
+    items[4 * i + 0] = v[i].a;
+    items[4 * i + 1] = v[i].b;
+    items[4 * i + 2] = v[i].c;
+    items[4 * i + 3] = v[i].d;
+  }
+  return VA_OK;
+}

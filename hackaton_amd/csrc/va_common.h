@@ -1,0 +1,128 @@
+// Shared device helpers for the gfx950 varlen attention kernels: element types, the
+// v_mfma_f32_32x32x16_{f16,bf16} wrappers, the lane <-> row maps of a 32x32 MFMA block and the
+// XOR swizzles of the LDS tiles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "va_kernels.h"
+
+namespace va {
+
+constexpr int kWave = 64;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element tag: 16-bit storage, fp32 arithmetic.
+struct F16 {
+  static constexpr int kId = 0;
+  __device__ static inline float to_f32(uint16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+  __device__ static inline uint16_t from_f32(float x) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct BF16 {
+  static constexpr int kId = 1;
+  __device__ static inline float to_f32(uint16_t x) {
+    return __builtin_bit_cast(float, (uint32_t)x << 16);
+  }
+  __device__ static inline uint16_t from_f32(float x) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <class E>
+__device__ inline uint32_t pack2(float lo, float hi) {
+  return (uint32_t)E::from_f32(lo) | ((uint32_t)E::from_f32(hi) << 16);
+}
+
+// Eight fp32 values -> one MFMA operand register quad (8 x 16-bit).
+template <class E>
+__device__ inline u32x4 pack8(float a0, float a1, float a2, float a3, float a4, float a5,
+                              float a6, float a7) {
+  u32x4 r;
+  r[0] = pack2<E>(a0, a1);
+  r[1] = pack2<E>(a2, a3);
+  r[2] = pack2<E>(a4, a5);
+  r[3] = pack2<E>(a6, a7);
+  return r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// 32x32x16 MFMA block layout (64 lanes, lane = 32 * hi + l32):
+//   A operand (32 rows x 16 k): lane supplies row l32, k slots [8 hi, 8 hi + 8)
+//   B operand (16 k x 32 cols): lane supplies col l32, k slots [8 hi, 8 hi + 8)
+//   C/D (32 x 32, 16 fp32 per lane): register j holds row 8 (j >> 2) + 4 hi + (j & 3), col l32
+// The k order inside one MFMA is free as long as A and B agree, so every operand that is a
+// reduction axis of the next product is loaded with rows permuted by `perm32`: then register j
+// of lane half hi holds logical row `reg_row(j, hi)` = 16 (j >> 3) + 8 hi + (j & 7), i.e. the 8
+// registers [8c, 8c + 8) are 8 consecutive rows, exactly the k slots of the next MFMA.
+// ---------------------------------------------------------------------------------------------
+__device__ __host__ inline int perm32(int r) {  // physical row r = 8g + 4h + i -> logical row
+  const int g = r >> 3, h = (r >> 2) & 1, i = r & 3;
+  return 16 * (g >> 1) + 8 * h + 4 * (g & 1) + i;
+}
+__device__ __host__ inline int reg_row(int j, int hi) { return 16 * (j >> 3) + 8 * hi + (j & 7); }
+
+// LDS tiles are arrays of 16-byte chunks (8 elements). Row-major tiles of 128 columns hold 16
+// chunks per row; the chunk index is XORed with `swz8(row)` so that the 8 rows one group of 8
+// lanes reads through perm32 ({b..b+3, b+8..b+11}) land in 8 different bank quads, and so that
+// rows written by the coalesced global->LDS copies spread too.
+__device__ inline int swz8(int r) {
+  return ((r & 3) | (((r >> 3) & 1) << 2)) ^ ((r >> 4) & 7);
+}
+// Tiles with 4 chunks per row (32 columns): 2 rows share one bank sweep.
+__device__ inline int swz4(int r) {
+  return (((r >> 1) & 1) | (((r >> 3) & 1) << 1)) ^ ((r >> 4) & 3);
+}
+
+// Element offset of (row, col) in a tile with `CHUNKS` 16-byte chunks per row.
+template <int CHUNKS>
+__device__ inline int tile_off(int row, int col) {
+  static_assert(CHUNKS == 4 || CHUNKS == 8 || CHUNKS == 16, "tile width");
+  const int chunk = col >> 3;
+  int sw;
+  if constexpr (CHUNKS == 4) sw = swz4(row);
+  else sw = swz8(row);
+  return row * (CHUNKS * 8) + (((chunk ^ sw) & (CHUNKS - 1)) << 3) + (col & 7);
+}
+
+__device__ inline u32x4 lds_read16(const uint16_t* base, int elem_off) {
+  return *reinterpret_cast<const u32x4*>(base + elem_off);
+}
+__device__ inline void lds_write16(uint16_t* base, int elem_off, u32x4 v) {
+  *reinterpret_cast<u32x4*>(base + elem_off) = v;
+}
+
+__device__ inline u32x4 gload16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline void gstore16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+__device__ inline uint16_t half_of(const u32x4& v, int e) {
+  const uint32_t w = v[e >> 1];
+  return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+}  // namespace va

@@ -1,0 +1,88 @@
+// Host-side launch descriptors shared by the kernel translation units and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace va {
+
+constexpr int kHeadDim = 128;  // Qwen2.5-1.5B / 7B head size; the kernels are built for it
+
+// Tile geometry; the plan builder (plan.cpp) emits work items for exactly these shapes.
+constexpr int kFwdWaves = 4;                 // forward: 32 queries per wave
+constexpr int kFwdBlockM = 32 * kFwdWaves;   // queries per forward work item
+constexpr int kBwdWaves = 4;                 // backward: 32 keys per wave
+constexpr int kBwdBlockN = 32 * kBwdWaves;   // keys per backward work item
+constexpr int kBwdBlockQ = 32;               // queries per backward inner step
+
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* lse;
+  const int32_t* items;  // int4 per work item: {q0, doc_end, doc_start, head}
+  int64_t n_items;
+  int64_t n_tokens;
+  int hq, hkv;
+  float scale;
+  int dtype;
+  hipStream_t stream;
+};
+
+struct BwdArgs {
+  const void* dout;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const float* lse;
+  const int32_t* items;  // int4 per work item: {k0, doc_end, head_begin, head_count}
+  int64_t n_items;
+  int64_t n_tokens;
+  int hq, hkv;
+  float scale;
+  int dtype;
+  float* delta;    // (hq, n_tokens)
+  float* dq_acc;   // (n_tokens, hq, 128)
+  float* dk_acc;   // (n_tokens, hkv, 128)
+  float* dv_acc;   // (n_tokens, hkv, 128)
+  void* dq;        // outputs in the element type, or null to keep the fp32 accumulators only
+  void* dk;
+  void* dv;
+  hipStream_t stream;
+};
+
+struct RopeArgs {
+  const void* x0;        // forward: q, k, v projections; backward: gradients
+  const void* x1;
+  const void* x2;
+  const float* cos;      // (1 or B, T, D) fp32
+  const float* sin;
+  int64_t cos_batch_stride;  // 0 when cos has one row of tables
+  int64_t cos_seq_stride;
+  const int32_t* b_idx;
+  const int32_t* t_idx;
+  void* y0;
+  void* y1;
+  void* y2;
+  int64_t n_tokens;
+  int heads, kv_heads;
+  int seq;               // padded layout: T
+  int in_dtype;          // dtype of x (0 f16, 1 bf16, 2 f32)
+  int out_dtype;         // dtype of y
+  int layout;            // 0 packed (N, H, D); 1 padded (B, H, T, D)
+  int expand;            // 1: write K/V for every query head (reference qkv_rotate semantics)
+  hipStream_t stream;
+};
+
+hipError_t launch_fwd(const FwdArgs& a);
+hipError_t launch_bwd(const BwdArgs& a);
+hipError_t launch_bwd_stage(const BwdArgs& a, int stage);  // 0 prepare, 1 main, 2 finish
+hipError_t launch_rope_fwd(const RopeArgs& a);
+hipError_t launch_rope_bwd(const RopeArgs& a);
+hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t* t_idx,
+                            int64_t n_tokens, int heads, int seq, int row_bytes, int mode,
+                            hipStream_t stream);
+
+}  // namespace va

@@ -1,0 +1,131 @@
+/*
+ * varlen_attn.h - C ABI of the MI355X (gfx950) packed variable-length causal GQA attention.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, launches asynchronously on
+ * the caller's HIP stream (`stream` is a hipStream_t, NULL = default stream), never allocates and
+ * never synchronises. Device buffers are owned by the caller. Return value: 0 on success, a
+ * negative VA_E* code for an argument error (nothing launched), or a positive hipError_t when a
+ * launch failed; `va_last_error()` describes the last failure of the calling thread.
+ *
+ * Layouts (row-major, contiguous, 16-byte aligned):
+ *   q, out, dq      (N, Hq, 128)   16-bit (dtype VA_F16 or VA_BF16)
+ *   k, v, dk, dv    (N, Hkv, 128)  16-bit; GQA: query head h reads key/value head h / (Hq/Hkv)
+ *   lse, delta      (Hq, N)        fp32, natural-log log-sum-exp of each query row
+ *   cu_seqlens      (n_docs + 1)   int32 host array, cu[0] = 0, non-decreasing; document i is
+ *                                  rows [cu[i], cu[i+1]) of the packed token axis
+ *   work items      int32 x 4 each, built on the host by va_plan_build and copied to the device
+ *
+ * Reference interfaces replaced (mergentlegen/hackaton, solution/attention.py):
+ *   va_plan_build       _cu_seqlens (195-209) + the tile walk inside the aten kernel
+ *   va_fwd              torch.ops.aten._efficient_attention_forward(q, k, v, None, cu, cu,
+ *                       max_len, max_len, 0.0, 1, True, scale=) at 221-222 (causal top-left,
+ *                       log-sum-exp returned)
+ *   va_bwd              torch.ops.aten._efficient_attention_backward(grad, q, k, v, None, out, cu,
+ *                       cu, max_len, max_len, lse, 0.0, seed, offset, 1, False, scale=) at
+ *                       230-232, plus the GQA sum of dk/dv of qkv_kernel mode 1 (113-134)
+ *   va_rope_fwd         qkv_kernel mode 0 (_qkv_forward, 36-83; launched at 168-170)
+ *   va_rope_bwd         qkv_kernel mode 1 (_qkv_backward, 86-134; launched at 185-187)
+ *   va_pack_rows        pack_kernel (288-300; launched at 311-312 and 323-324)
+ */
+#ifndef VARLEN_ATTN_H_
+#define VARLEN_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  VA_OK = 0,
+  VA_EINVAL = -1,    /* null pointer, negative size, misaligned buffer, bad enum value */
+  VA_ESHAPE = -2,    /* head_dim != 128, Hq not a multiple of Hkv, sizes out of range */
+  VA_EDTYPE = -3,    /* unsupported element type */
+  VA_ESEQ = -4,      /* cu_seqlens not starting at 0, decreasing, or beyond the token count */
+  VA_ECAPACITY = -5  /* output buffer too small (plan items, workspace) */
+};
+
+enum { VA_F16 = 0, VA_BF16 = 1, VA_F32 = 2 };
+enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1 };
+enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
+enum { VA_BWD_PREPARE = 0, VA_BWD_MAIN = 1, VA_BWD_FINISH = 2 };
+
+const char* va_last_error(void);
+int32_t va_abi_version(void);
+int32_t va_head_dim(void);
+
+/* ---- work plan (host only; no GPU call) ------------------------------------------------------
+ * Work items for the forward (kind VA_PLAN_FWD: one per 128-query tile x query head) or the
+ * backward (VA_PLAN_BWD: one per 128-key tile x query head) over the documents of cu_seqlens,
+ * ordered longest first. Fully masked causal tiles and cross-document tiles never appear.
+ * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
+int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
+                 int64_t* n_items);
+int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
+                  int32_t* items, int64_t capacity, int64_t* n_items);
+
+/* ---- attention forward ------------------------------------------------------------------------
+ * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row.
+ * Replaces: solution/attention.py:221-222 (aten::_efficient_attention_forward). */
+int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+           const int32_t* items, int64_t n_items, int64_t total_tokens, int32_t hq, int32_t hkv,
+           int32_t head_dim, float scale, int32_t dtype, void* stream);
+
+/* ---- attention backward -----------------------------------------------------------------------
+ * Workspace: delta (Hq, N) fp32 and fp32 accumulators dq (N, Hq, 128), dk, dv (N, Hkv, 128),
+ * at the byte offsets va_bwd_workspace_layout reports. dq/dk/dv may be NULL: the fp32
+ * accumulators in the workspace are then the result (read them at the reported offsets).
+ * Replaces: solution/attention.py:230-232 (aten::_efficient_attention_backward) and the GQA
+ * reduction of dk/dv at solution/attention.py:113-134. */
+int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim,
+                            int64_t offsets[4], int64_t* bytes);
+int va_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,
+           const float* lse, const int32_t* items, int64_t n_items, int64_t total_tokens,
+           int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype, void* dq,
+           void* dk, void* dv, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The same backward in its three launches, for callers that time or overlap them separately:
+ * prepare (delta = rowsum(dO * O), clears the accumulators), main (dQ/dK/dV accumulation), finish
+ * (casts the accumulators to dq/dk/dv; nothing when they are NULL). Same arguments as va_bwd.
+ * Replaces: the same reference call as va_bwd (solution/attention.py:230-232). */
+int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k, const void* v,
+                 const void* out, const float* lse, const int32_t* items, int64_t n_items,
+                 int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim, float scale,
+                 int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
+/* ---- rotary embedding -------------------------------------------------------------------------
+ * Forward: q (N, heads*D), k, v (N, kv_heads*D) in in_dtype (VA_F16/VA_BF16/VA_F32); cos, sin
+ * fp32 tables indexed at b*cos_batch_stride + t*cos_seq_stride (b, t from b_idx/t_idx, int32).
+ * Rotation in fp32, rounded once to out_dtype. layout VA_LAYOUT_PACKED writes (N, H, D),
+ * VA_LAYOUT_PADDED writes (B, H, seq, D) (caller zero-fills). expand=1 writes K/V for all `heads`
+ * (reference qkv_rotate semantics); expand=0 keeps kv_heads (GQA-native attention input).
+ * Backward: the inverse rotation (and the sum of the G copies when expand=1); dq/dk/dv read in
+ * in_dtype from `layout`, written (N, H*D) in out_dtype.
+ * Replaces: solution/attention.py:36-134 (qkv_kernel modes 0 and 1). */
+int va_rope_fwd(const void* q, const void* k, const void* v, const float* cos, const float* sin,
+                int64_t cos_batch_stride, int64_t cos_seq_stride, const int32_t* b_idx,
+                const int32_t* t_idx, void* q_out, void* k_out, void* v_out, int64_t n_tokens,
+                int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t seq, int32_t in_dtype,
+                int32_t out_dtype, int32_t layout, int32_t expand, void* stream);
+int va_rope_bwd(const void* dq, const void* dk, const void* dv, const float* cos,
+                const float* sin, int64_t cos_batch_stride, int64_t cos_seq_stride,
+                const int32_t* b_idx, const int32_t* t_idx, void* dq_in, void* dk_in,
+                void* dv_in, int64_t n_tokens, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                int32_t seq, int32_t in_dtype, int32_t out_dtype, int32_t layout, int32_t expand,
+                void* stream);
+
+/* ---- row packing ------------------------------------------------------------------------------
+ * mode 0: (B, heads, seq, head_dim) -> (N, heads*head_dim) rows of the real tokens (exact);
+ * mode 1: the reverse scatter into a caller-zeroed (B, heads, seq, head_dim) buffer.
+ * Replaces: solution/attention.py:288-300 (pack_kernel). */
+int va_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t* t_idx,
+                 int64_t n_tokens, int32_t heads, int32_t seq, int32_t head_dim,
+                 int32_t elem_bytes, int32_t mode, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VARLEN_ATTN_H_ */

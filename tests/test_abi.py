@@ -1,0 +1,137 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/varlen_attn.h declares,
+plans work correctly and rejects bad arguments before any GPU call."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from hackaton_amd import _lib
+from hackaton_amd.attention import build_plan_host
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "varlen_attn.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(va_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+    assert lib.va_abi_version() == 1
+    assert lib.va_head_dim() == 128
+
+
+def plan(lengths, hq, hkv, kind):
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    return cu, build_plan_host(cu, hq, hkv, kind)
+
+
+@pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1, 1, 1], [129, 0, 300],
+                                     [4096, 17]])
+@pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (12, 12)])
+def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
+    cu, items = plan(lengths, hq, hkv, _lib.VA_PLAN_FWD)
+    seen = set()
+    for q0, doc_end, doc_start, h in items.tolist():
+        assert 0 <= h < hq
+        d = int(np.searchsorted(cu, doc_start, side="right")) - 1
+        assert cu[d] == doc_start and cu[d + 1] == doc_end  # never crosses a document
+        assert doc_start <= q0 < doc_end and (q0 - doc_start) % 128 == 0
+        seen.add((q0, h))
+    expected = {(q0, h) for s, e in zip(cu[:-1], cu[1:]) for q0 in range(s, e, 128)
+                for h in range(hq)}
+    assert seen == expected and len(items) == len(expected)
+    # longest first: keys visited per tile never increase along the list
+    work = [min(q0 + 128, e) - s for q0, e, s, _ in items.tolist()]
+    assert work == sorted(work, reverse=True)
+
+
+@pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1], [257, 3]])
+def test_backward_plan_covers_every_key_tile_once(lengths):
+    hq, hkv = 12, 2
+    cu, items = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
+    seen = set()
+    for k0, doc_end, h0, count in items.tolist():
+        assert count == 1 and 0 <= h0 < hq
+        d = int(np.searchsorted(cu, k0, side="right")) - 1
+        assert cu[d + 1] == doc_end and (k0 - cu[d]) % 128 == 0
+        seen.add((k0, h0))
+    expected = {(k0, h) for s, e in zip(cu[:-1], cu[1:]) for k0 in range(s, e, 128)
+                for h in range(hq)}
+    assert seen == expected and len(items) == len(expected)
+
+
+def test_plan_rejects_bad_cu_seqlens():
+    lib = _lib.lib()
+    n = ctypes.c_int64()
+    for cu, code in (([1, 5], _lib.VA_ESEQ), ([0, 5, 3], _lib.VA_ESEQ)):
+        arr = np.asarray(cu, dtype=np.int32)
+        rc = lib.va_plan_size(arr.ctypes.data_as(_lib._pi32), len(cu) - 1, 12, 2, 0,
+                              ctypes.byref(n))
+        assert rc == code
+        assert b"cu_seqlens" in lib.va_last_error()
+    arr = np.asarray([0, 5], dtype=np.int32)
+    assert lib.va_plan_size(arr.ctypes.data_as(_lib._pi32), 1, 12, 5, 0,
+                            ctypes.byref(n)) == _lib.VA_ESHAPE
+    assert lib.va_plan_size(arr.ctypes.data_as(_lib._pi32), 1, 12, 2, 7,
+                            ctypes.byref(n)) == _lib.VA_EINVAL
+    small = np.zeros((1, 4), dtype=np.int32)
+    rc = lib.va_plan_build(arr.ctypes.data_as(_lib._pi32), 1, 12, 2, 0,
+                           small.ctypes.data_as(_lib._pi32), 1, ctypes.byref(n))
+    assert rc == _lib.VA_ECAPACITY and n.value == 12
+
+
+def test_attention_entry_points_validate_before_launching():
+    """Argument errors come back as codes with a message; no GPU is touched."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    rc = lib.va_fwd(fake, fake, fake, fake, fake, fake, 4, 100, 12, 2, 64, 0.1, 0, None)
+    assert rc == _lib.VA_ESHAPE and b"head_dim" in lib.va_last_error()
+    rc = lib.va_fwd(fake, fake, fake, fake, fake, fake, 4, 100, 12, 5, 128, 0.1, 0, None)
+    assert rc == _lib.VA_ESHAPE
+    rc = lib.va_fwd(fake, fake, fake, fake, fake, fake, 4, 100, 12, 2, 128, 0.1, 9, None)
+    assert rc == _lib.VA_EDTYPE
+    rc = lib.va_fwd(fake, None, fake, fake, fake, fake, 4, 100, 12, 2, 128, 0.1, 0, None)
+    assert rc == _lib.VA_EINVAL
+    rc = lib.va_fwd(fake, ctypes.c_void_p(0x1008), fake, fake, fake, fake, 4, 100, 12, 2, 128,
+                    0.1, 0, None)
+    assert rc == _lib.VA_EINVAL and b"aligned" in lib.va_last_error()
+    rc = lib.va_fwd(fake, fake, fake, fake, fake, fake, 4, 100, 12, 2, 128, float("nan"), 0,
+                    None)
+    assert rc == _lib.VA_EINVAL
+    # nothing to do is not an error
+    assert lib.va_fwd(None, None, None, None, None, None, 0, 0, 12, 2, 128, 0.1, 0, None) == 0
+    offs = (ctypes.c_int64 * 4)()
+    nbytes = ctypes.c_int64()
+    assert lib.va_bwd_workspace_layout(2048, 12, 2, 128, offs, ctypes.byref(nbytes)) == 0
+    assert list(offs) == [0, 98304, 98304 + 2048 * 12 * 512, 98304 + 2048 * 12 * 512
+                          + 2048 * 2 * 512]
+    assert nbytes.value == offs[3] + 2048 * 2 * 512
+    rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, None,
+                    None, None, fake, nbytes.value - 1, None)
+    assert rc == _lib.VA_ECAPACITY
+    rc = lib.va_rope_fwd(fake, fake, fake, fake, fake, 0, 128, fake, fake, fake, fake, fake, 10,
+                         12, 2, 128, 0, 0, 0, 1, 0, None)
+    assert rc == _lib.VA_EINVAL  # padded layout needs seq > 0
+    rc = lib.va_pack_rows(fake, fake, fake, fake, 10, 12, 64, 127, 2, 0, None)
+    assert rc == _lib.VA_ESHAPE
+
+
+def test_product_path_refuses_cpu_tensors():
+    import torch
+
+    from hackaton_amd import varlen_attention
+    q = torch.zeros(8, 12, 128, dtype=torch.float16)
+    k = torch.zeros(8, 2, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU only"):
+        varlen_attention(q, k, k, [8], 0.1)
