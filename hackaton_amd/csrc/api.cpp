@@ -70,7 +70,8 @@ extern "C" int va_fwd(const void* q, const void* k, const void* v, void* out, fl
   if (rc) return rc;
   if ((rc = check_dtype16(dtype))) return rc;
   if (n_items < 0 || n_items > INT32_MAX) return va::fail(VA_EINVAL, "n_items out of range");
-  if (!std::isfinite(scale)) return va::fail(VA_EINVAL, "scale is not finite");
+  if (!std::isfinite(scale) || scale <= 0.f)
+    return va::fail(VA_EINVAL, "scale must be finite and positive");
   if (n_items == 0 || total_tokens == 0) return VA_OK;
   if ((rc = check_ptrs({q, k, v, out, lse, items}, "va_fwd"))) return rc;
   va::FwdArgs a{q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, scale, dtype,
@@ -110,7 +111,8 @@ int bwd_common(int32_t stage, const void* dout, const void* q, const void* k, co
   if ((rc = check_dtype16(dtype))) return rc;
   if (stage < -1 || stage > VA_BWD_FINISH) return va::fail(VA_EINVAL, "bad stage %d", stage);
   if (n_items < 0 || n_items > INT32_MAX) return va::fail(VA_EINVAL, "n_items out of range");
-  if (!std::isfinite(scale)) return va::fail(VA_EINVAL, "scale is not finite");
+  if (!std::isfinite(scale) || scale <= 0.f)
+    return va::fail(VA_EINVAL, "scale must be finite and positive");
   int64_t offs[4], need = 0;
   va_bwd_workspace_layout(total_tokens, hq, hkv, head_dim, offs, &need);
   if (total_tokens == 0) return VA_OK;

@@ -63,74 +63,108 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(
 // ---------------------------------------------------------------------------------------------
 // Main backward kernel.
 // ---------------------------------------------------------------------------------------------
-template <class E, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void bwd_kernel(
+namespace bwd {
+constexpr int NW = kBwdWaves;   // waves, 32 keys each
+constexpr int BN = 32 * NW;     // keys per work item
+constexpr int BQ = kBwdBlockQ;  // queries per step
+constexpr int D = kHeadDim;
+constexpr int LD = D + 8;       // row stride (halfs) of the Q, dO and K tiles
+constexpr int LDT = BQ + 16;    // row stride (halfs) of the dS^T tile (rows = keys)
+constexpr int NT = NW * 64;
+constexpr int QTILE = BQ * LD;
+// LDS map (halfs): Q[2 stages], dO[2 stages], K, dS^T; then lse2/delta floats [2 stages][BQ].
+constexpr int OFF_Q = 0;
+constexpr int OFF_DO = OFF_Q + 2 * QTILE;
+constexpr int OFF_K = OFF_DO + 2 * QTILE;
+constexpr int OFF_DST = OFF_K + BN * LD;
+constexpr int HALFS = OFF_DST + BN * LDT;
+constexpr int STAGE_CHUNKS = 2 * BQ * 16;        // Q and dO 16-byte chunks per step
+constexpr int SPT = STAGE_CHUNKS / NT;            // per thread
+static_assert(SPT * NT == STAGE_CHUNKS, "staging split");
+}  // namespace bwd
+
+template <class E>
+__global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dq_acc,
     float* __restrict__ dk_acc, float* __restrict__ dv_acc, const int4* __restrict__ items,
     int n_tokens, int hq, int hkv, float scale, float scale_log2) {
-  constexpr int BN = 32 * NW;    // keys per work item
-  constexpr int BQ = kBwdBlockQ; // queries per step
-  constexpr int D = kHeadDim;
-  constexpr int NT = NW * 64;
-  constexpr int NCH = BN / 8;    // 16-byte chunks per row of the dS and K^T tiles
-  static_assert(BQ == 32, "the query step is one 32-row MFMA block");
-  static_assert(4 % NW == 0 || NW % 4 == 0, "d blocks per wave");
-
-  __shared__ __attribute__((aligned(16))) uint16_t qs[BQ * D];     // Q rows, swz8
-  __shared__ __attribute__((aligned(16))) uint16_t qt[D * BQ];     // Q^T rows (d), swz4
-  __shared__ __attribute__((aligned(16))) uint16_t dos[BQ * D];    // dO rows
-  __shared__ __attribute__((aligned(16))) uint16_t dot_[D * BQ];   // dO^T rows (d)
-  __shared__ __attribute__((aligned(16))) uint16_t dss[BQ * BN];   // dS rows (query), keys
-  __shared__ __attribute__((aligned(16))) uint16_t kt[D * BN];     // K^T rows (d), keys
-  __shared__ __attribute__((aligned(16))) float lse_s[BQ];
-  __shared__ __attribute__((aligned(16))) float del_s[BQ];
+  using namespace bwd;
+  __shared__ __attribute__((aligned(16))) uint16_t smem_raw[HALFS];
+  __shared__ __attribute__((aligned(16))) float stat_raw[2][2][BQ];  // [stage][lse2 | delta][row]
+  lds_u16* smem = (lds_u16*)smem_raw;
 
   const int4 it = items[blockIdx.x];
   const int k0 = it.x, doc_end = it.y, h_begin = it.z, h_count = it.w;
   const int group = hq / hkv;
   const int kvh = h_begin / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int src = lane & 15, grp = lane >> 4;
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
 
   const int kw0 = k0 + 32 * wave;   // first key of this wave
   const int my_key = kw0 + l32;
-  const bool key_valid = my_key < doc_end;
-  const bool wave_live = kw0 < doc_end;
 
-  // K and V of this lane's key as MFMA B operands (k slots = d).
+  // K and V of this lane's key as MFMA B operands (column = key, k slots = d), rows clamped.
   u32x4 kf[8], vf[8];
   {
-    const uint16_t* kp = k + (long)(key_valid ? my_key : k0) * kvrow + kvh * D + 8 * hi;
-    const uint16_t* vp = v + (long)(key_valid ? my_key : k0) * kvrow + kvh * D + 8 * hi;
+    const long row = min(my_key, doc_end - 1);
+    const uint16_t* kp = k + row * kvrow + kvh * D + 8 * hi;
+    const uint16_t* vp = v + row * kvrow + kvh * D + 8 * hi;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      kf[kk] = key_valid ? gload16(kp + 16 * kk) : u32x4{0, 0, 0, 0};
-      vf[kk] = key_valid ? gload16(vp + 16 * kk) : u32x4{0, 0, 0, 0};
+      kf[kk] = gload16(kp + 16 * kk);
+      vf[kk] = gload16(vp + 16 * kk);
     }
   }
-  // K^T of the whole key tile in LDS (B operand of dQ = dS K).
+  // The key tile, row-major, in LDS (B operand of dQ = dS K through transposed reads).
   {
-    constexpr int UNITS = (BN / 4) * 16;
-    for (int u = tid; u < UNITS; u += NT) {
-      const int kq = u >> 4, col8 = u & 15;
-      u32x4 r4[4];
+    const int srow = tid >> 4, scol = 8 * (tid & 15);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 4 * kq + r;
-        r4[r] = key < doc_end ? gload16(k + (long)key * kvrow + kvh * D + 8 * col8)
-                              : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x2 w;
-        w[0] = (uint32_t)half_of(r4[0], e) | ((uint32_t)half_of(r4[1], e) << 16);
-        w[1] = (uint32_t)half_of(r4[2], e) | ((uint32_t)half_of(r4[3], e) << 16);
-        *reinterpret_cast<u32x2*>(kt + tile_off<NCH>(8 * col8 + e, 4 * kq)) = w;
-      }
+    for (int i = 0; i < BN / 16; ++i) {
+      const long row = min(k0 + srow + 16 * i, doc_end - 1);
+      st128(smem + OFF_K + (srow + 16 * i) * LD + scol,
+            gload16(k + row * kvrow + kvh * D + scol));
     }
   }
+
+  // Staging of one query step (Q and dO rows, lse * log2e and delta) through registers.
+  const int s_tensor = tid / (NT / 2);              // threads [0, NT/2): Q, the rest: dO
+  const int s_unit = tid % (NT / 2);
+  const int s_row = s_unit >> 4, s_col = 8 * (s_unit & 15);
+  constexpr int SROWS = (NT / 2) / 16;              // rows covered per staging pass
+  u32x4 sreg[SPT];
+  float st_lse = 0.f, st_del = 0.f;
+  auto gload_step = [&](int h, int qs0) {
+    const uint16_t* base = (s_tensor ? dout : q) + h * D + s_col;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      const long row = min(qs0 + s_row + SROWS * i, doc_end - 1);
+      sreg[i] = gload16(base + row * qrow);
+    }
+    if (tid < BQ) {
+      const int row = qs0 + tid;
+      const bool ok = row < doc_end;
+      st_lse = ok ? lse[(long)h * n_tokens + row] * kLog2e : INFINITY;
+      st_del = ok ? delta[(long)h * n_tokens + row] : 0.f;
+    }
+  };
+  auto store_step = [&](int stage) {
+    lds_u16* base = smem + (s_tensor ? OFF_DO : OFF_Q) + stage * QTILE + s_row * LD + s_col;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) st128(base + SROWS * i * LD, sreg[i]);
+    if (tid < BQ) {
+      stat_raw[stage][0][tid] = st_lse;
+      stat_raw[stage][1][tid] = st_del;
+    }
+  };
+
+  // Per-lane LDS read bases (halfs).
+  const int rm_read = perm32(l32) * LD + 8 * hi;                              // rows = queries
+  const int tr_read = (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) + 4 * (src & 3);
+  const int dst_read = OFF_DST + (8 * hi + 2 * (src >> 2)) * LDT + 16 * (grp & 1) + 4 * (src & 3);
+  const int dst_write = OFF_DST + (32 * wave + l32) * LDT + 8 * hi;
 
   f32x16 dkacc[4], dvacc[4];
 #pragma unroll
@@ -139,137 +173,114 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_kernel(
     dvacc[db] = f32x16{};
   }
 
-  for (int hh = 0; hh < h_count; ++hh) {
-    const int h = h_begin + hh;
-    for (int qs0 = k0; qs0 < doc_end; qs0 += BQ) {
-      __syncthreads();  // the previous step's readers of qs/qt/dos/dot/dss/lse_s are done
-      // Stage Q and dO rows [qs0, qs0 + 32) of head h: row-major and transposed.
-      for (int u = tid; u < 2 * (BQ / 4) * 16; u += NT) {
-        const int which = u >> 7;            // 0: Q, 1: dO
-        const int unit = u & 127;
-        const int qq = unit >> 4, col8 = unit & 15;
-        const uint16_t* src = which ? dout : q;
-        u32x4 r4[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = qs0 + 4 * qq + r;
-          r4[r] = row < doc_end ? gload16(src + (long)row * qrow + h * D + 8 * col8)
-                                : u32x4{0, 0, 0, 0};
-        }
-        uint16_t* rm = which ? dos : qs;
-        uint16_t* tr = which ? dot_ : qt;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) lds_write16(rm, tile_off<16>(4 * qq + r, 8 * col8), r4[r]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          u32x2 w;
-          w[0] = (uint32_t)half_of(r4[0], e) | ((uint32_t)half_of(r4[1], e) << 16);
-          w[1] = (uint32_t)half_of(r4[2], e) | ((uint32_t)half_of(r4[3], e) << 16);
-          *reinterpret_cast<u32x2*>(tr + tile_off<4>(8 * col8 + e, 4 * qq)) = w;
-        }
-      }
-      if (tid < BQ) {
-        const int row = qs0 + tid;
-        const bool ok = row < doc_end;
-        lse_s[tid] = ok ? lse[(long)h * n_tokens + row] * kLog2e : INFINITY;
-        del_s[tid] = ok ? delta[(long)h * n_tokens + row] : 0.f;
-      }
-      __syncthreads();
+  // The (head, query step) sequence of this work item.
+  const int steps_per_head = (doc_end - k0 + BQ - 1) / BQ;
+  const int n_steps = steps_per_head * h_count;
+  auto step_head = [&](int s) { return h_begin + s / steps_per_head; };
+  auto step_q0 = [&](int s) { return k0 + (s % steps_per_head) * BQ; };
 
-      const bool active = wave_live && kw0 <= qs0 + BQ - 1;
-      if (active) {
-        f32x16 sacc = f32x16{}, pacc = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const int off = tile_off<16>(perm32(l32), 16 * kk + 8 * hi);
-          sacc = E::mfma(lds_read16(qs, off), kf[kk], sacc);
-          pacc = E::mfma(lds_read16(dos, off), vf[kk], pacc);
-        }
-        // register j <-> query qs0 + reg_row(j, hi), key my_key
-        const bool diag = kw0 + 31 > qs0;
-        float p[16], ds[16];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int r0 = 16 * c + 8 * hi;
-          const f32x4 l0 = *reinterpret_cast<const f32x4*>(lse_s + r0);
-          const f32x4 l1 = *reinterpret_cast<const f32x4*>(lse_s + r0 + 4);
-          const f32x4 d0 = *reinterpret_cast<const f32x4*>(del_s + r0);
-          const f32x4 d1 = *reinterpret_cast<const f32x4*>(del_s + r0 + 4);
-#pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const int j = 8 * c + s;
-            const float lv = s < 4 ? l0[s] : l1[s - 4];
-            const float dv = s < 4 ? d0[s] : d1[s - 4];
-            float pv = fast_exp2(sacc[j] * scale_log2 - lv);
-            if (diag && my_key > qs0 + r0 + s) pv = 0.f;
-            p[j] = pv;
-            ds[j] = pv * (pacc[j] - dv);
-          }
-        }
-        u32x4 pp[2], dsp[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int j0 = 8 * c;
-          pp[c] = pack8<E>(p[j0], p[j0 + 1], p[j0 + 2], p[j0 + 3], p[j0 + 4], p[j0 + 5],
-                           p[j0 + 6], p[j0 + 7]);
-          dsp[c] = pack8<E>(ds[j0], ds[j0 + 1], ds[j0 + 2], ds[j0 + 3], ds[j0 + 4], ds[j0 + 5],
-                            ds[j0 + 6], ds[j0 + 7]);
-        }
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const int off = tile_off<4>(32 * db + perm32(l32), 16 * c + 8 * hi);
-            dvacc[db] = E::mfma(pp[c], lds_read16(dot_, off), dvacc[db]);
-            dkacc[db] = E::mfma(dsp[c], lds_read16(qt, off), dkacc[db]);
-          }
-        }
-        // dS (queries x keys) to LDS, in the element type (the precision the MFMA consumes).
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          dss[tile_off<NCH>(reg_row(j, hi), 32 * wave + l32)] = E::from_f32(ds[j]);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) dss[tile_off<NCH>(reg_row(j, hi), 32 * wave + l32)] = 0;
-      }
-      __syncthreads();
+  gload_step(step_head(0), step_q0(0));
+  store_step(0);
+  if (n_steps > 1) gload_step(step_head(1), step_q0(1));
+  __syncthreads();
 
-      // dQ rows [qs0, qs0 + 32) = dS (32 x BN) . K (BN x 128): each wave owns 128 / NW columns.
-      constexpr int DB_PER_WAVE = 4 / NW > 0 ? 4 / NW : 1;
-      if (wave < 4) {
+  for (int s = 0; s < n_steps; ++s) {
+    const int stage = s & 1;
+    const int h = step_head(s), qs0 = step_q0(s);
+    const lds_u16* qs = smem + OFF_Q + stage * QTILE;
+    const lds_u16* dos = smem + OFF_DO + stage * QTILE;
+
+    // S = Q K^T and dP = dO V^T (rows = queries, columns = this wave's keys).
+    f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
-        for (int i = 0; i < DB_PER_WAVE; ++i) {
-          const int db = wave * DB_PER_WAVE + i;
-          f32x16 acc = f32x16{};
+    for (int kk = 0; kk < 8; ++kk) {
+      sacc = E::mfma(ld128(qs + rm_read + 16 * kk), kf[kk], sacc);
+      pacc = E::mfma(ld128(dos + rm_read + 16 * kk), vf[kk], pacc);
+    }
+    // register j <-> query qs0 + reg_row(j, hi) = qs0 + 16 (j >> 3) + 8 hi + (j & 7).
+    float p[16], ds[16];
 #pragma unroll
-          for (int kc = 0; kc < BN / 16; ++kc) {
-            const u32x4 a = lds_read16(dss, tile_off<NCH>(perm32(l32), 16 * kc + 8 * hi));
-            const u32x4 b = lds_read16(kt, tile_off<NCH>(32 * db + perm32(l32), 16 * kc + 8 * hi));
-            acc = E::mfma(a, b, acc);
-          }
-          float* dqp = dq_acc + (long)h * D + 32 * db + perm32(l32);
+    for (int c = 0; c < 2; ++c) {
+      const int r0 = 16 * c + 8 * hi;
+      const lds_f32x4* st = reinterpret_cast<const lds_f32x4*>(
+          (__attribute__((address_space(3))) float*)&stat_raw[stage][0][0]);
+      const f32x4 l0 = st[r0 / 4], l1 = st[r0 / 4 + 1];
+      const f32x4 d0 = st[(BQ + r0) / 4], d1 = st[(BQ + r0) / 4 + 1];
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int row = qs0 + reg_row(j, hi);
-            if (row < doc_end) atomicAdd(dqp + (long)row * qrow, acc[j] * scale);
-          }
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int j = 8 * c + e;
+        const float lv = e < 4 ? l0[e] : l1[e - 4];
+        p[j] = fast_exp2(fmaf(sacc[j], scale_log2, -lv));
+        ds[j] = e < 4 ? d0[e] : d1[e - 4];
       }
     }
+    if (kw0 + 31 > qs0) {  // the step crosses this wave's diagonal: key > query -> P = 0
+      const int lim = my_key - qs0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (reg_row(j, hi) < lim) p[j] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ds[j] = p[j] * (pacc[j] - ds[j]);
+
+    // dV += P^T dO and dK += dS^T Q: A = this lane's key row (k = queries), B via tr reads.
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const u32x4 pa = pack8_tr<E>(p + 8 * c);
+      const u32x4 da = pack8_tr<E>(ds + 8 * c);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int off = tr_read + 16 * c * LD + 32 * db;
+        dvacc[db] = E::mfma(pa, ldtr8(dos + off, LD), dvacc[db]);
+        dkacc[db] = E::mfma(da, ldtr8(qs + off, LD), dkacc[db]);
+      }
+    }
+    // dS^T rows (this lane's key), queries in natural order.
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int j0 = 8 * c;
+      st128(smem + dst_write + 16 * c,
+            pack8<E>(ds[j0], ds[j0 + 1], ds[j0 + 2], ds[j0 + 3], ds[j0 + 4], ds[j0 + 5],
+                     ds[j0 + 6], ds[j0 + 7]));
+    }
+    // Next step's Q/dO into the other stage (its readers finished before the last barrier).
+    if (s + 1 < n_steps) {
+      store_step(stage ^ 1);
+      if (s + 2 < n_steps) gload_step(step_head(s + 2), step_q0(s + 2));
+    }
+    __syncthreads();
+
+    // dQ rows [qs0, qs0 + 32), columns [32 w, 32 w + 32) = dS (32 x BN) K (BN x 32).
+    {
+      f32x16 acc = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < BN / 16; ++kc) {
+        const u32x4 a = ldtr8(smem + dst_read + 16 * kc * LDT, LDT);
+        const u32x4 b = ldtr8(smem + OFF_K + tr_read + 16 * kc * LD + 32 * wave, LD);
+        acc = E::mfma(a, b, acc);
+      }
+      // register j <-> query qs0 + 8 (j >> 2) + 4 hi + (j & 3), column 32 w + l32.
+      float* dqp = dq_acc + (long)qs0 * qrow + (long)h * D + 32 * wave + l32;
+      const int rows_left = doc_end - qs0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = 8 * (j >> 2) + 4 * hi + (j & 3);
+        if (r < rows_left) atomicAdd(dqp + (long)r * qrow, acc[j] * scale);
+      }
+    }
+    __syncthreads();
   }
 
-  // dK, dV of this wave's keys: register j <-> key kw0 + 8 (j >> 2) + 4 hi + (j & 3),
-  // column d = 32 db + perm32(l32).
-  if (wave_live) {
+  // dK, dV of this wave's keys: register j <-> key kw0 + 8 (j >> 2) + 4 hi + (j & 3), column
+  // d = 32 db + l32.
+  if (kw0 < doc_end) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const int d = 32 * db + perm32(l32);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int key = kw0 + 8 * (j >> 2) + 4 * hi + (j & 3);
         if (key < doc_end) {
-          const long off = ((long)key * hkv + kvh) * D + d;
+          const long off = ((long)key * hkv + kvh) * D + 32 * db + l32;
           atomicAdd(dk_acc + off, dkacc[db][j] * scale);
           atomicAdd(dv_acc + off, dvacc[db][j]);
         }
@@ -304,7 +315,7 @@ static hipError_t launch_bwd_prepare_t(const BwdArgs& a) {
 template <class E>
 static hipError_t launch_bwd_main_t(const BwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
-  hipLaunchKernelGGL((bwd_kernel<E, kBwdWaves>), dim3((unsigned)a.n_items), dim3(kBwdWaves * 64),
+  hipLaunchKernelGGL((bwd_kernel<E>), dim3((unsigned)a.n_items), dim3(bwd::NT),
                      0, a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.dout, a.lse, a.delta, a.dq_acc,
                      a.dk_acc, a.dv_acc, (const int4*)a.items, (int)a.n_tokens, a.hq, a.hkv,

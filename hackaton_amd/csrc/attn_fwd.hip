@@ -1,208 +1,221 @@
 // Forward kernel of packed varlen causal GQA attention for gfx950.
 //
-// One work-group = one work item of the plan: NW waves x 32 queries of one document and one query
-// head. The K/V tiles of the document (BN = 64 keys) stream through LDS (double buffered, K
-// row-major, V transposed so the P.V product reads 8 consecutive keys per lane); Q stays in
-// registers. Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16 so that one lane owns one
-// query: the online softmax (running max / sum, exp2 with scale*log2(e) folded in) is in-lane plus
-// one cross-half exchange. O^T = V^T P^T accumulates in fp32; per-row log-sum-exp is written to
-// lse[h][token] (natural log). Causal masking is applied only on tiles that cross the diagonal;
-// tiles past the diagonal are never loaded (the plan bounds the key range by the last query).
+// One work-group = one work item of the plan: 128 queries (4 strips of 32) of one document and one
+// query head, run by 8 waves in two halves. Half h (waves 4h .. 4h + 3) processes the key tiles
+// t = h, h + 2, h + 4, ... (64 keys each) for the 4 query strips, so two waves share each SIMD:
+// one wave's MFMAs overlap the other's softmax, LDS waits and barrier skew, and the key range of
+// the work item is split in two. At the end half 1 hands its unnormalised (O, m, l) to half 0
+// through LDS and half 0 merges, normalises and writes O and the log-sum-exp.
+//
+// Per wave: Q stays in registers as the MFMA B operand; S^T = K Q^T (v_mfma_f32_32x32x16) puts
+// one query per lane, so the online softmax is in-lane plus one v_permlane32_swap; O^T += V^T P^T
+// reads V^T straight from the row-major tile with ds_read_b64_tr_b16. K/V tiles stream through
+// two LDS stages of tile pairs (plain row-major copies, row stride 136 halfs); the next pair's
+// global loads are in flight while the current pair is computed, one barrier per pair. The
+// running maximum is exact, so the dominant probability of a peaky row is exactly 1 in the 16-bit
+// P operand. Rows past the document end are clamped to its last row (finite) and masked.
 #include "va_common.h"
 #include "va_kernels.h"
 
 namespace va {
 
-constexpr int kFwdBN = 64;
+namespace fwd {
+constexpr int NS = 4;           // query strips of 32 per work item
+constexpr int BM = 32 * NS;     // queries per work item
+constexpr int NW = 2 * NS;      // waves: two halves over the key tiles
+constexpr int NT = NW * 64;
+constexpr int BN = 64;          // keys per tile
+constexpr int D = kHeadDim;
+constexpr int LD = D + 8;       // LDS row stride (halfs) of the K and V tiles
+constexpr int TILE = BN * LD;   // halfs per K or V tile
+constexpr int PAIR = 4 * TILE;  // K0, V0, K1, V1 of one tile pair
+constexpr int LPT = 4 * BN * 16 / NT;  // 16-byte staging chunks per thread per pair
+static_assert(LPT * NT == 4 * BN * 16, "pair staging split");
+static_assert(BM == kFwdBlockM, "the plan's query tile");
+}  // namespace fwd
 
-template <class E, int NW>
-__global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(
+template <class E>
+__global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
     const int4* __restrict__ items, int n_tokens, int hq, int hkv, float scale_log2) {
-  constexpr int BM = 32 * NW;
-  constexpr int BN = kFwdBN;
-  constexpr int D = kHeadDim;
-  constexpr int NT = NW * 64;
-  constexpr int KCH = BN * 16 / NT;    // 16-byte K chunks per thread per tile
-  constexpr int VU = (BN / 4) * 16 / NT;  // (key quad, d chunk) units per thread per tile
-  static_assert(KCH * NT == BN * 16 && VU * NT == (BN / 4) * 16, "tile split");
-
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][BN * D];  // K rows, 16 chunks, swz8
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][D * BN];  // V^T rows (d), 8 chunks
+  using namespace fwd;
+  __shared__ __attribute__((aligned(16))) uint16_t smem_raw[2 * PAIR];
+  lds_u16* smem = (lds_u16*)smem_raw;
 
   const int4 it = items[blockIdx.x];
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w;
   const int group = hq / hkv;
   const int kvh = h / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int half = wave / NS, strip = wave % NS;
+  const int src = lane & 15, grp = lane >> 4;   // transposed-read group and source lane
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
 
-  const int wq0 = q0 + 32 * wave;             // first query of this wave
+  const int wq0 = q0 + 32 * strip;
   const int my_q = wq0 + l32;
   const bool q_valid = my_q < doc_end;
-  const bool wave_live = wq0 < doc_end;
 
+  // Q fragment: B operand of S^T = K Q^T (column = this lane's query, k slots = d).
   u32x4 qf[8];
   {
-    const uint16_t* qp = q + (long)(q_valid ? my_q : q0) * qrow + h * D + 8 * hi;
+    const uint16_t* qp = q + (long)min(my_q, doc_end - 1) * qrow + h * D + 8 * hi;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      qf[kk] = q_valid ? gload16(qp + 16 * kk) : u32x4{0, 0, 0, 0};
-    }
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = gload16(qp + 16 * kk);
   }
 
   const int kv_end = min(q0 + BM, doc_end);
   const int n_tiles = (kv_end - doc_start + BN - 1) / BN;
+  const int n_pairs = (n_tiles + 1) / 2;
 
-  u32x4 kreg[KCH];
-  u32x4 vreg[VU][4];
-  const uint16_t* kbase = k + kvh * D;
-  const uint16_t* vbase = v + kvh * D;
-
-  auto load_tile = [&](int t) {
-    const int kv0 = doc_start + t * BN;
+  // Staging of one tile pair: chunk i of this thread is tile (i >> 2), tensor ((i >> 1) & 1),
+  // row (tid >> 4) + 32 (i & 1), 16-byte column (tid & 15). Rows clamped to the document.
+  const int srow = tid >> 4, scol = 8 * (tid & 15);
+  const uint16_t* kbase = k + kvh * D + scol;
+  const uint16_t* vbase = v + kvh * D + scol;
+  u32x4 sr[LPT];
+  auto gload_pair = [&](int p) {
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * NT;
-      const int key = kv0 + (c >> 4);
-      kreg[i] = key < doc_end ? gload16(kbase + (long)key * kvrow + 8 * (c & 15))
-                              : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < VU; ++i) {
-      const int u = tid + i * NT;
-      const int key = kv0 + 4 * (u >> 4);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        vreg[i][r] = key + r < doc_end
-                         ? gload16(vbase + (long)(key + r) * kvrow + 8 * (u & 15))
-                         : u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < LPT; ++i) {
+      const int t = 2 * p + (i >> 2);
+      const long row = min(doc_start + t * BN + srow + 32 * (i & 1), doc_end - 1);
+      sr[i] = gload16((((i >> 1) & 1) ? vbase : kbase) + row * kvrow);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_pair = [&](int stage) {
+    lds_u16* base = smem + stage * PAIR + srow * LD + scol;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * NT;
-      lds_write16(ks[buf], tile_off<16>(c >> 4, 8 * (c & 15)), kreg[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < VU; ++i) {
-      const int u = tid + i * NT;
-      const int kq = u >> 4, col8 = u & 15;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x2 w;
-        w[0] = (uint32_t)half_of(vreg[i][0], e) | ((uint32_t)half_of(vreg[i][1], e) << 16);
-        w[1] = (uint32_t)half_of(vreg[i][2], e) | ((uint32_t)half_of(vreg[i][3], e) << 16);
-        *reinterpret_cast<u32x2*>(vt[buf] + tile_off<8>(8 * col8 + e, 4 * kq)) = w;
-      }
+    for (int i = 0; i < LPT; ++i) {
+      st128(base + ((i >> 2) * 2 + ((i >> 1) & 1)) * TILE + 32 * (i & 1) * LD, sr[i]);
     }
   };
+
+  // Per-lane LDS read bases (halfs) inside this half's K / V tile of a stage.
+  const int kread = 2 * half * TILE + perm32(l32) * LD + 8 * hi;     // K rows, k = d
+  const int vread = (2 * half + 1) * TILE + (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1)
+                    + 4 * ((((src & 3) & 1) << 1) | ((src & 3) >> 1));  // V^T via tr reads
 
   f32x16 oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
+  // One 64-key tile for this wave: S^T, mask, online softmax, O^T += V^T P^T.
+  auto tile = [&](int stage, int t) {
     const int kv0 = doc_start + t * BN;
-    if (t + 1 < n_tiles) load_tile(t + 1);
-
-    if (wave_live && kv0 <= wq0 + 31) {
-      f32x16 sacc[2];
+    const lds_u16* kb = smem + stage * PAIR + kread;
+    f32x16 s[2];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        sacc[b] = f32x16{};
+    for (int b = 0; b < 2; ++b) {
+      s[b] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const u32x4 a = lds_read16(ks[buf], tile_off<16>(32 * b + perm32(l32), 16 * kk + 8 * hi));
-          sacc[b] = E::mfma(a, qf[kk], sacc[b]);
-        }
-      }
-      const bool diag = kv0 + BN - 1 > wq0;
-      float mt = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float x = sacc[b][j] * scale_log2;
-          if (diag && kv0 + 32 * b + reg_row(j, hi) > my_q) x = -INFINITY;
-          sacc[b][j] = x;
-          mt = fmaxf(mt, x);
-        }
-      }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run, mt);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      float rs = 0.f;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float p = fast_exp2(sacc[b][j] - m_use);
-          sacc[b][j] = p;
-          rs += p;
-        }
-      }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
-
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int j0 = 8 * c;
-          const u32x4 pf = pack8<E>(sacc[b][j0], sacc[b][j0 + 1], sacc[b][j0 + 2], sacc[b][j0 + 3],
-                                    sacc[b][j0 + 4], sacc[b][j0 + 5], sacc[b][j0 + 6],
-                                    sacc[b][j0 + 7]);
-#pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const u32x4 a = lds_read16(vt[buf], tile_off<8>(32 * db + perm32(l32),
-                                                            32 * b + 16 * c + 8 * hi));
-            oacc[db] = E::mfma(a, pf, oacc[db]);
-          }
-        }
-      }
+      for (int kk = 0; kk < 8; ++kk) s[b] = E::mfma(ld128(kb + 32 * b * LD + 16 * kk), qf[kk], s[b]);
     }
+    if (kv0 + BN - 1 > wq0) {  // the tile crosses this strip's diagonal: key > query -> -inf
+      const int lim = my_q - kv0;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (32 * b + reg_row(j, hi) > lim) s[b][j] = -INFINITY;
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mt = fmaxf(mt, s[b][j]);
+    mt = max_with_other_half(mt) * scale_log2;
+    const float m_new = fmaxf(m_run, mt);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked first tile
+    const float alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    float rs = 0.f;
+    u32x4 pf[2][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(s[b][8 * c + e], scale_log2, -m_use));
+        pf[b][c] = pack8_tr<E>(p);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) rs = E::sum2(pf[b][c][w], rs);
+      }
+    l_run = l_run * alpha + rs;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    const lds_u16* vb = smem + stage * PAIR + vread;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const u32x4 a = ldtr8(vb + (32 * b + 16 * c) * LD + 32 * db, LD);
+          oacc[db] = E::mfma(a, pf[b][c], oacc[db]);
+        }
+  };
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+  gload_pair(0);
+  store_pair(0);
+  __syncthreads();
+  for (int p = 0; p < n_pairs; ++p) {
+    const int stage = p & 1;
+    if (p + 1 < n_pairs) gload_pair(p + 1);
+    const int t = 2 * p + half;
+    // Tiles entirely past this strip's diagonal are skipped (their P would be all zero).
+    if (t < n_tiles && doc_start + t * BN <= wq0 + 31) tile(stage, t);
+    if (p + 1 < n_pairs) store_pair(stage ^ 1);
     __syncthreads();
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  // Merge the two halves through LDS: half 1 publishes (O, m, l) in its lane order, which is
+  // the same (query, d) order as the partner wave of half 0.
+  float* xo = reinterpret_cast<float*>(smem_raw);          // [strip][64 reg][64 lanes]
+  float* xs = xo + NS * 64 * 64;                            // [strip][2][64 lanes]
+  if (half == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xo[(strip * 64 + 16 * db + j) * 64 + lane] = oacc[db][j];
+    xs[(strip * 2 + 0) * 64 + lane] = m_run;
+    xs[(strip * 2 + 1) * 64 + lane] = l_run;
+  }
+  __syncthreads();
+  if (half == 1) return;
+  const float m_b = xs[(strip * 2 + 0) * 64 + lane];
+  const float l_b = xs[(strip * 2 + 1) * 64 + lane];
+  const float m_tot = fmaxf(m_run, m_b);
+  const float m_use = m_tot == -INFINITY ? 0.f : m_tot;
+  const float sa = fast_exp2(m_run - m_use), sb = fast_exp2(m_b - m_use);
+  const float l_tot = sum_with_other_half(l_run * sa + l_b * sb);
   if (q_valid) {
     const float inv = 1.f / l_tot;
+    const float ca = sa * inv, cb = sb * inv;
     uint16_t* op = o + (long)my_q * qrow + h * D;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
+      float x[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        x[j] = oacc[db][j] * ca + xo[(strip * 64 + 16 * db + j) * 64 + lane] * cb;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int j0 = 8 * c;
-        const f32x16& a = oacc[db];
-        const u32x4 w = pack8<E>(a[j0] * inv, a[j0 + 1] * inv, a[j0 + 2] * inv, a[j0 + 3] * inv,
-                                 a[j0 + 4] * inv, a[j0 + 5] * inv, a[j0 + 6] * inv,
-                                 a[j0 + 7] * inv);
+        const u32x4 w = pack8<E>(x[j0], x[j0 + 1], x[j0 + 2], x[j0 + 3], x[j0 + 4], x[j0 + 5],
+                                 x[j0 + 6], x[j0 + 7]);
         gstore16(op + 32 * db + 16 * c + 8 * hi, w);
       }
     }
-    if (hi == 0) lse[(long)h * n_tokens + my_q] = (m_run + fast_log2(l_tot)) * kLn2;
+    if (hi == 0) lse[(long)h * n_tokens + my_q] = (m_tot + fast_log2(l_tot)) * kLn2;
   }
 }
 
-template <class E, int NW>
+template <class E>
 static hipError_t launch_fwd_t(const FwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
-  hipLaunchKernelGGL((fwd_kernel<E, NW>), dim3((unsigned)a.n_items), dim3(NW * 64), 0, a.stream,
+  hipLaunchKernelGGL((fwd_kernel<E>), dim3((unsigned)a.n_items), dim3(fwd::NT), 0, a.stream,
                      (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
                      (uint16_t*)a.out, a.lse, (const int4*)a.items, (int)a.n_tokens, a.hq, a.hkv,
                      a.scale * kLog2e);
@@ -210,7 +223,7 @@ static hipError_t launch_fwd_t(const FwdArgs& a) {
 }
 
 hipError_t launch_fwd(const FwdArgs& a) {
-  return a.dtype == 0 ? launch_fwd_t<F16, kFwdWaves>(a) : launch_fwd_t<BF16, kFwdWaves>(a);
+  return a.dtype == 0 ? launch_fwd_t<F16>(a) : launch_fwd_t<BF16>(a);
 }
 
 }  // namespace va

@@ -19,6 +19,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 // Element tag: 16-bit storage, fp32 arithmetic.
 struct F16 {
   static constexpr int kId = 0;
@@ -31,6 +34,10 @@ struct F16 {
   __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // acc + the two 16-bit values packed in x (v_dot2_f32_f16 with (1, 1)).
+  __device__ static inline float sum2(uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), f16x2_t{1, 1}, acc, false);
   }
 };
 
@@ -46,11 +53,26 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // acc + the two 16-bit values packed in x (v_dot2_f32_bf16 with (1, 1)).
+  __device__ static inline float sum2(uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), bf16x2_t{1, 1}, acc,
+                                           false);
+  }
 };
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> one register of two 16-bit values, round to nearest even
+// (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 on gfx950).
 template <class E>
 __device__ inline uint32_t pack2(float lo, float hi) {
-  return (uint32_t)E::from_f32(lo) | ((uint32_t)E::from_f32(hi) << 16);
+  if constexpr (E::kId == 0) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  }
 }
 
 // Eight fp32 values -> one MFMA operand register quad (8 x 16-bit).
@@ -63,6 +85,28 @@ __device__ inline u32x4 pack8(float a0, float a1, float a2, float a3, float a4, 
   r[2] = pack2<E>(a4, a5);
   r[3] = pack2<E>(a6, a7);
   return r;
+}
+
+// Value of lane (l ^ 32) combined with this lane's own. v_permlane32_swap exchanges the upper 32
+// lanes of its first operand with the lower 32 lanes of its second: with both holding x, lane l
+// ends up with {x[l], x[l ^ 32]} across the two registers. The instruction is emitted through
+// inline asm (with the 2 wait states a VALU-written source needs): the compiler's model of the
+// intrinsic treats the two results as interchangeable and drops one of them.
+__device__ inline void swap_halves(float x, float& r0, float& r1) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ inline float max_with_other_half(float x) {
+  float r0, r1;
+  swap_halves(x, r0, r1);
+  return fmaxf(r0, r1);
+}
+__device__ inline float sum_with_other_half(float x) {
+  float r0, r1;
+  swap_halves(x, r0, r1);
+  return r0 + r1;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -104,6 +148,41 @@ __device__ inline int tile_off(int row, int col) {
   return row * (CHUNKS * 8) + (((chunk ^ sw) & (CHUNKS - 1)) << 3) + (col & 7);
 }
 
+// ---------------------------------------------------------------------------------------------
+// LDS access through address-space-3 pointers, so that per-lane bases plus compile-time offsets
+// fold into the ds instruction's immediate offset.
+//
+// ds_read_b64_tr_b16 (gfx950 transposed read): within each group of 16 lanes, source lane i reads
+// 4 consecutive 16-bit values at its address; destination lane j receives element (j & 3) of the
+// values read by source lanes 4e + (j >> 2), e = 0..3. With source lane i pointing at row
+// (r0 + 2 (i >> 2)) and columns [c0 + 4 (i & 3), +4), lane j receives column c0 + j of the 4 rows
+// r0, r0 + 2, r0 + 4, r0 + 6: a column of a row-major tile, i.e. 4 k slots of an MFMA operand
+// whose k axis runs along the tile's rows. Two such reads (r0 and r0 + 1) give the 8 k slots of
+// one 32x32x16 operand in the slot order {0, 2, 4, 6, 1, 3, 5, 7}.
+// ---------------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ inline u32x4 ld128(const lds_u16* p) { return *reinterpret_cast<const lds_u32x4*>(p); }
+__device__ inline void st128(lds_u16* p, u32x4 v) { *reinterpret_cast<lds_u32x4*>(p) = v; }
+__device__ inline u32x2 ldtr(const lds_u16* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (lds_s16x4*)const_cast<lds_u16*>(p)));
+}
+// One 8-slot operand from two transposed reads at rows r0 (slots 0,2,4,6) and r0 + 1 (1,3,5,7).
+__device__ inline u32x4 ldtr8(const lds_u16* p_r0, int row_stride) {
+  const u32x2 a = ldtr(p_r0), b = ldtr(p_r0 + row_stride);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+// Register operand in the matching slot order: values v[0..7] of 8 consecutive k indices.
+template <class E>
+__device__ inline u32x4 pack8_tr(const float* v) {
+  return pack8<E>(v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]);
+}
+
 __device__ inline u32x4 lds_read16(const uint16_t* base, int elem_off) {
   return *reinterpret_cast<const u32x4*>(base + elem_off);
 }
@@ -120,6 +199,11 @@ __device__ inline uint16_t half_of(const u32x4& v, int e) {
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier (LLVM AMDGPU IGroupLP).
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020,
+              kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
+#define VA_SCHED(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 constexpr float kLog2e = 1.4426950408889634f;

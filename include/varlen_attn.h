@@ -66,7 +66,8 @@ int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t
                   int32_t* items, int64_t capacity, int64_t* n_items);
 
 /* ---- attention forward ------------------------------------------------------------------------
- * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row.
+ * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row;
+ * scale must be finite and > 0 (D^-0.5 in the reference).
  * Replaces: solution/attention.py:221-222 (aten::_efficient_attention_forward). */
 int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
            const int32_t* items, int64_t n_items, int64_t total_tokens, int32_t hq, int32_t hkv,

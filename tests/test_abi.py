@@ -109,6 +109,8 @@ def test_attention_entry_points_validate_before_launching():
     rc = lib.va_fwd(fake, fake, fake, fake, fake, fake, 4, 100, 12, 2, 128, float("nan"), 0,
                     None)
     assert rc == _lib.VA_EINVAL
+    rc = lib.va_fwd(fake, fake, fake, fake, fake, fake, 4, 100, 12, 2, 128, -0.5, 0, None)
+    assert rc == _lib.VA_EINVAL and b"positive" in lib.va_last_error()
     # nothing to do is not an error
     assert lib.va_fwd(None, None, None, None, None, None, 0, 0, 12, 2, 128, 0.1, 0, None) == 0
     offs = (ctypes.c_int64 * 4)()
