@@ -163,7 +163,6 @@ def main():
         b.record()
 
     def bwd_main_launch(s, stream, a, b):
-        bwd(s, stream.cuda_stream, _lib.VA_BWD_PREPARE)
         a.record()
         bwd(s, stream.cuda_stream, _lib.VA_BWD_MAIN)
         b.record()

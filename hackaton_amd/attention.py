@@ -15,8 +15,9 @@ Differences that keep the drop-in contract:
 * `varlen_attention` accepts key/value with Hkv heads (GQA-native: the kernels read each key/value
   head once for its G query heads) as well as the reference's expanded Hq-head form.
 * `packed_attention` rotates q and k without expanding K/V to the query heads and runs the
-  attention on Hkv key/value heads; the backward sums dK/dV over each GQA group inside the
-  attention kernel (fp32) and applies the inverse rotation straight from the fp32 accumulators.
+  attention on Hkv key/value heads; the backward kernels write dQ and per-query-head dK/dV, and
+  the inverse rotation sums the G heads of each group in fp32 (the reference sums its expanded
+  fp16 copies the same way, solution/attention.py:113-134). The backward is deterministic.
 * fp16 and bf16 inputs both run on the MFMA kernels (the reference computes in fp16 only).
 
 Every op requires the HIP library and CUDA (HIP) tensors; there is no other implementation.
@@ -156,7 +157,8 @@ def attention_forward(query, key, value, plan, scale):
 
 
 def bwd_workspace(n, hq, hkv, device):
-    offsets = np.zeros(4, dtype=np.int64)
+    """Workspace of the backward (per-query-head dK/dV partials) and its byte offsets."""
+    offsets = np.zeros(2, dtype=np.int64)
     nbytes = np.zeros(1, dtype=np.int64)
     check(lib().va_bwd_workspace_layout(n, hq, hkv, HEAD_DIM, offsets.ctypes.data_as(_lib._pi64),
                                         nbytes.ctypes.data_as(_lib._pi64)),
@@ -165,8 +167,9 @@ def bwd_workspace(n, hq, hkv, device):
 
 
 def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=True):
-    """dq, dk, dv (dk/dv summed over each GQA group). With outputs=False returns the fp32
-    accumulators (N, Hq, D), (N, Hkv, D), (N, Hkv, D) that live in the workspace."""
+    """dq, dk, dv of packed causal attention (dk/dv summed over each GQA group), deterministic.
+    With outputs=False returns dq and the per-query-head dK/dV partials (N, Hq, D) in the element
+    type (plus the workspace that holds them), for a caller that sums them itself."""
     n, hq, d = query.shape
     hkv = key.shape[1]
     dtype = _attn_dtype(query)
@@ -174,22 +177,26 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
     if grad.dtype != query.dtype:
         grad = grad.to(query.dtype)
     grad = grad.contiguous()
-    ws, offs = bwd_workspace(n, hq, hkv, query.device)
+    dq = torch.empty_like(query)
     if outputs:
-        dq, dk, dv = torch.empty_like(query), torch.empty_like(key), torch.empty_like(value)
+        dk, dv = torch.empty_like(key), torch.empty_like(value)
+        ws, offs = (bwd_workspace(n, hq, hkv, query.device) if hq != hkv
+                    else (torch.empty(0, dtype=torch.uint8, device=query.device), [0, 0]))
     else:
-        dq = dk = dv = None
+        dk = dv = None
+        ws, offs = bwd_workspace(n, hq, hkv, query.device)
     check(lib().va_bwd(_ptr(grad), _ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
                        _ptr(plan.bwd_items), plan.n_bwd, n, hq, hkv, d, float(scale), dtype,
-                       _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(), _stream()), "va_bwd")
+                       _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws) if ws.numel() else None,
+                       ws.numel(), _stream()), "va_bwd")
     if outputs:
         return dq, dk, dv
+    part = n * hq * d * 2
 
-    def view(off, shape):
-        count = int(np.prod(shape))
-        return ws[off: off + 4 * count].view(torch.float32).view(*shape)
+    def view(off):
+        return ws[off: off + part].view(query.dtype).view(n, hq, d)
 
-    return view(offs[1], (n, hq, d)), view(offs[2], (n, hkv, d)), view(offs[3], (n, hkv, d)), ws
+    return dq, view(offs[0]), view(offs[1]), ws
 
 
 class VarlenAttention(torch.autograd.Function):
@@ -363,10 +370,12 @@ class PackedAttention(torch.autograd.Function):
         seq, heads, kv_heads, lengths, scale = ctx.meta
         out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
                                                kv_heads, lengths, scale)
-        dq_acc, dk_acc, dv_acc, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
+        # dq and the per-query-head dK/dV partials; the inverse rotation sums the partials over
+        # each GQA group (as solution/attention.py:113-134 sums its expanded copies)
+        dq_r, dk_part, dv_part, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
                                                          outputs=False)
-        dq, dk, dv = rope_backward(dq_acc, dk_acc, dv_acc, cos, sin, b_idx, t_idx, heads,
-                                   kv_heads, q.dtype)
+        dq, dk, dv = rope_backward(dq_r, dk_part, dv_part, cos, sin, b_idx, t_idx, heads,
+                                   kv_heads, q.dtype, expand=True)
         grads = (dq, dk.to(k.dtype), dv.to(v.dtype))
         return (*grads, None, None, None, None, None, None, None, None, None, None)
 

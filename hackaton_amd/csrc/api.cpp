@@ -81,21 +81,14 @@ extern "C" int va_fwd(const void* q, const void* k, const void* v, void* out, fl
 }
 
 extern "C" int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t hkv,
-                                       int32_t head_dim, int64_t offsets[4], int64_t* bytes) {
+                                       int32_t head_dim, int64_t offsets[2], int64_t* bytes) {
   int rc = check_attn_shape(total_tokens, hq, hkv, head_dim);
   if (rc) return rc;
   if (offsets == nullptr || bytes == nullptr) return va::fail(VA_EINVAL, "NULL output");
-  const int64_t n = total_tokens;
-  int64_t off = 0;
-  offsets[0] = off;  // delta (Hq, N)
-  off += round256(n * hq * 4);
-  offsets[1] = off;  // dq accumulator (N, Hq, D)
-  off += round256(n * hq * head_dim * 4);
-  offsets[2] = off;  // dk accumulator (N, Hkv, D)
-  off += round256(n * hkv * head_dim * 4);
-  offsets[3] = off;  // dv accumulator (N, Hkv, D)
-  off += round256(n * hkv * head_dim * 4);
-  *bytes = off;
+  const int64_t part = round256(total_tokens * hq * head_dim * 2);
+  offsets[0] = 0;     // per-query-head dK partials (N, Hq, D), element type
+  offsets[1] = part;  // per-query-head dV partials
+  *bytes = 2 * part;
   return VA_OK;
 }
 
@@ -109,25 +102,28 @@ int bwd_common(int32_t stage, const void* dout, const void* q, const void* k, co
   int rc = check_attn_shape(total_tokens, hq, hkv, head_dim);
   if (rc) return rc;
   if ((rc = check_dtype16(dtype))) return rc;
-  if (stage < -1 || stage > VA_BWD_FINISH) return va::fail(VA_EINVAL, "bad stage %d", stage);
   if (n_items < 0 || n_items > INT32_MAX) return va::fail(VA_EINVAL, "n_items out of range");
   if (!std::isfinite(scale) || scale <= 0.f)
     return va::fail(VA_EINVAL, "scale must be finite and positive");
-  int64_t offs[4], need = 0;
+  if ((dk == nullptr) != (dv == nullptr))
+    return va::fail(VA_EINVAL, "va_bwd: dk and dv must both be given or both be NULL");
+  // With Hq == Hkv and outputs given, the per-head dK/dV are the outputs: no workspace needed.
+  const bool direct = dk != nullptr && hq == hkv;
+  int64_t offs[2], need = 0;
   va_bwd_workspace_layout(total_tokens, hq, hkv, head_dim, offs, &need);
   if (total_tokens == 0) return VA_OK;
-  if (workspace_bytes < need)
+  if (!direct && workspace_bytes < need)
     return va::fail(VA_ECAPACITY, "workspace %lld bytes, need %lld", (long long)workspace_bytes,
                     (long long)need);
-  if ((rc = check_ptrs({dout, q, k, v, out, lse, workspace}, "va_bwd"))) return rc;
+  if ((rc = check_ptrs({dout, q, k, v, out, lse, dq}, "va_bwd"))) return rc;
   if (n_items > 0 && (rc = check_ptrs({items}, "va_bwd items"))) return rc;
-  const bool any_out = dq || dk || dv;
-  if (any_out && (rc = check_ptrs({dq, dk, dv}, "va_bwd outputs"))) return rc;
+  if (dk != nullptr && (rc = check_ptrs({dk, dv}, "va_bwd outputs"))) return rc;
+  if (!direct && (rc = check_ptrs({workspace}, "va_bwd workspace"))) return rc;
   char* ws = static_cast<char*>(workspace);
+  void* dk_part = direct ? dk : static_cast<void*>(ws + offs[0]);
+  void* dv_part = direct ? dv : static_cast<void*>(ws + offs[1]);
   va::BwdArgs a{dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, scale, dtype,
-                reinterpret_cast<float*>(ws + offs[0]), reinterpret_cast<float*>(ws + offs[1]),
-                reinterpret_cast<float*>(ws + offs[2]), reinterpret_cast<float*>(ws + offs[3]),
-                dq, dk, dv, (hipStream_t)stream};
+                dq, dk_part, dv_part, dk, dv, (hipStream_t)stream};
   hipError_t e = stage < 0 ? va::launch_bwd(a) : va::launch_bwd_stage(a, stage);
   return e == hipSuccess ? VA_OK : hip_fail(e, "va_bwd launch");
 }

@@ -1,170 +1,132 @@
-// Backward kernels of packed varlen causal GQA attention for gfx950.
+// Backward of packed varlen causal GQA attention for gfx950: one atomic-free, deterministic launch
+// over two kinds of work items, plus the GQA sum of dK/dV when query heads share key/value heads.
 //
-//  bwd_pre_kernel    delta[h][t] = sum_d dO * O (fp32) and clears the fp32 dQ/dK/dV accumulators.
-//  bwd_kernel        one work-group = NW waves x 32 keys of one document (a key tile) and a run of
-//                    query heads of one GQA group. K and V of the wave's keys stay in registers;
-//                    for every 32-query step from the key tile's first key to the document end it
-//                    stages Q and dO (row-major and transposed) in LDS, recomputes
-//                    P = exp2(S scale log2e - lse log2e), and accumulates dV += P^T dO and
-//                    dK += dS^T Q in registers (dS = P (dP - delta), dP = dO V^T). dS goes through
-//                    LDS so the work-group computes dQ = dS K for its keys, added to the fp32 dQ
-//                    accumulator with global atomics. dK/dV are added once per work item to fp32
-//                    accumulators, which sums the query heads of a GQA group.
-//  bwd_post_kernel   casts the fp32 accumulators to the element type.
+//  kv item   128 keys of one document x one query head, 8 waves: 4 key strips of 32 x 2 halves
+//            that take alternate 32-query steps (two waves per SIMD). Per step: S = Q K^T and
+//            dP = dO V^T (rows = queries), P = exp2(S scale log2e - lse log2e), dS = P (dP - delta),
+//            dV += P^T dO and dK += dS^T Q with the transposed operands read by ds_read_b64_tr_b16.
+//            delta = rowsum(dO * O) is computed by the staging threads. The halves add their partial
+//            dK/dV through LDS and write them once, per query head: into dK/dV themselves when
+//            Hq == Hkv, else into per-head partials that the finish pass (or the rotary backward)
+//            sums over each GQA group, as the reference sums its expanded copies.
+//  q item    128 queries of one document x one query head, 8 waves: 4 query strips x 2 halves that
+//            take alternate 32-key tiles. Per tile: S^T = K Q^T and dP^T = V dO^T (one query per
+//            lane, lse and delta in-lane), dS^T, dQ^T += K^T dS^T. The halves add their dQ through
+//            LDS and write it once in the element type.
+//  finish    dK/dV = sum over the G query heads of each group of the per-head partials.
 #include "va_common.h"
 #include "va_kernels.h"
 
 namespace va {
 
-// ---------------------------------------------------------------------------------------------
-// delta + accumulator clear: 16 lanes per (token, head) row, 8 elements per lane.
-// ---------------------------------------------------------------------------------------------
-template <class E>
-__global__ __launch_bounds__(256) void bwd_pre_kernel(
-    const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout, float* __restrict__ delta,
-    float* __restrict__ dq_acc, float* __restrict__ dk_acc, float* __restrict__ dv_acc,
-    int n_tokens, int hq, int hkv) {
-  const long row = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  const long rows = (long)n_tokens * hq;
-  float acc = 0.f;
-  if (row < rows) {
-    const long t = row / hq;
-    const int h = (int)(row - t * hq);
-    const u32x4 a = gload16(o + row * kHeadDim + 8 * sub);
-    const u32x4 b = gload16(dout + row * kHeadDim + 8 * sub);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += E::to_f32(half_of(a, e)) * E::to_f32(half_of(b, e));
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    f32x4* dq4 = reinterpret_cast<f32x4*>(dq_acc + row * kHeadDim + 8 * sub);
-    dq4[0] = z;
-    dq4[1] = z;
-    if (h < hkv) {
-      const long kr = t * hkv + h;
-      f32x4* dk4 = reinterpret_cast<f32x4*>(dk_acc + kr * kHeadDim + 8 * sub);
-      f32x4* dv4 = reinterpret_cast<f32x4*>(dv_acc + kr * kHeadDim + 8 * sub);
-      dk4[0] = z;
-      dk4[1] = z;
-      dv4[0] = z;
-      dv4[1] = z;
-    }
-  }
-  acc += __shfl_xor(acc, 8, 16);
-  acc += __shfl_xor(acc, 4, 16);
-  acc += __shfl_xor(acc, 2, 16);
-  acc += __shfl_xor(acc, 1, 16);
-  if (row < rows && sub == 0) {
-    const long t = row / hq;
-    const int h = (int)(row - t * hq);
-    delta[(long)h * n_tokens + t] = acc;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Main backward kernel.
-// ---------------------------------------------------------------------------------------------
 namespace bwd {
-constexpr int NW = kBwdWaves;   // waves, 32 keys each
-constexpr int BN = 32 * NW;     // keys per work item
-constexpr int BQ = kBwdBlockQ;  // queries per step
-constexpr int D = kHeadDim;
-constexpr int LD = D + 8;       // row stride (halfs) of the Q, dO and K tiles
-constexpr int LDT = BQ + 16;    // row stride (halfs) of the dS^T tile (rows = keys)
+constexpr int NS = 4;           // strips of 32 per work item
+constexpr int NW = 2 * NS;      // two halves
 constexpr int NT = NW * 64;
-constexpr int QTILE = BQ * LD;
-// LDS map (halfs): Q[2 stages], dO[2 stages], K, dS^T; then lse2/delta floats [2 stages][BQ].
-constexpr int OFF_Q = 0;
-constexpr int OFF_DO = OFF_Q + 2 * QTILE;
-constexpr int OFF_K = OFF_DO + 2 * QTILE;
-constexpr int OFF_DST = OFF_K + BN * LD;
-constexpr int HALFS = OFF_DST + BN * LDT;
-constexpr int STAGE_CHUNKS = 2 * BQ * 16;        // Q and dO 16-byte chunks per step
-constexpr int SPT = STAGE_CHUNKS / NT;            // per thread
-static_assert(SPT * NT == STAGE_CHUNKS, "staging split");
+constexpr int D = kHeadDim;
+constexpr int LD = D + 8;       // row stride (halfs) of every row-major LDS tile
+constexpr int BK = 32 * NS;     // keys per kv item
+constexpr int BQ = 32;          // queries per kv-item step
+constexpr int QB = 32 * NS;     // queries per q item
+constexpr int BT = 32;          // keys per q-item tile
+constexpr int ROWT = 32 * LD;   // halfs of a 32-row tile
+// kv item LDS (halfs): K[128], V[128], Q[stage][half], dO[stage][half]; stats floats apart.
+constexpr int KV_OFF_K = 0;
+constexpr int KV_OFF_V = KV_OFF_K + BK * LD;
+constexpr int KV_OFF_Q = KV_OFF_V + BK * LD;
+constexpr int KV_OFF_DO = KV_OFF_Q + 4 * ROWT;
+constexpr int KV_HALFS = KV_OFF_DO + 4 * ROWT;
+// q item LDS (halfs): [stage][K0, V0, K1, V1] 32-row tiles.
+constexpr int Q_PAIR = 4 * ROWT;
+constexpr int Q_HALFS = 2 * Q_PAIR;
+constexpr int HALFS = KV_HALFS > Q_HALFS ? KV_HALFS : Q_HALFS;
+static_assert(BK == kBwdBlockN && QB == kBwdBlockM && BQ == kBwdBlockQ, "plan tile sizes");
+static_assert(NS * 128 * 64 * 4 <= HALFS * 2, "dK/dV exchange fits in LDS");
+constexpr int kKindKV = 0, kKindQ = 1;
 }  // namespace bwd
 
+// --------------------------------------------------------------------------------------------
+// kv item: dK, dV of 128 keys for one query head.
+// --------------------------------------------------------------------------------------------
 template <class E>
-__global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
+__device__ __forceinline__ void bwd_kv_item(
+    lds_u16* smem, float (&stat)[2][2][2][bwd::BQ], const int4 it,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint16_t* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dq_acc,
-    float* __restrict__ dk_acc, float* __restrict__ dv_acc, const int4* __restrict__ items,
-    int n_tokens, int hq, int hkv, float scale, float scale_log2) {
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ out,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+    uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part, int n_tokens, int hq,
+    int hkv, float scale, float scale_log2) {
   using namespace bwd;
-  __shared__ __attribute__((aligned(16))) uint16_t smem_raw[HALFS];
-  __shared__ __attribute__((aligned(16))) float stat_raw[2][2][BQ];  // [stage][lse2 | delta][row]
-  lds_u16* smem = (lds_u16*)smem_raw;
-
-  const int4 it = items[blockIdx.x];
-  const int k0 = it.x, doc_end = it.y, h_begin = it.z, h_count = it.w;
-  const int group = hq / hkv;
-  const int kvh = h_begin / group;
+  const int k0 = it.x, doc_end = it.y, h = it.w & 0xffffff;
+  const int kvh = h / (hq / hkv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int half = wave / NS, strip = wave % NS;
   const int src = lane & 15, grp = lane >> 4;
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
-
-  const int kw0 = k0 + 32 * wave;   // first key of this wave
+  const int kw0 = k0 + 32 * strip;
   const int my_key = kw0 + l32;
 
-  // K and V of this lane's key as MFMA B operands (column = key, k slots = d), rows clamped.
-  u32x4 kf[8], vf[8];
-  {
-    const long row = min(my_key, doc_end - 1);
-    const uint16_t* kp = k + row * kvrow + kvh * D + 8 * hi;
-    const uint16_t* vp = v + row * kvrow + kvh * D + 8 * hi;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      kf[kk] = gload16(kp + 16 * kk);
-      vf[kk] = gload16(vp + 16 * kk);
-    }
-  }
-  // The key tile, row-major, in LDS (B operand of dQ = dS K through transposed reads).
-  {
+  {  // K and V tiles, row-major, rows clamped to the document
     const int srow = tid >> 4, scol = 8 * (tid & 15);
 #pragma unroll
-    for (int i = 0; i < BN / 16; ++i) {
-      const long row = min(k0 + srow + 16 * i, doc_end - 1);
-      st128(smem + OFF_K + (srow + 16 * i) * LD + scol,
-            gload16(k + row * kvrow + kvh * D + scol));
+    for (int i = 0; i < BK / 32; ++i) {
+      const long g = (long)min(k0 + srow + 32 * i, doc_end - 1) * kvrow + kvh * D + scol;
+      st128(smem + KV_OFF_K + (srow + 32 * i) * LD + scol, gload16(k + g));
+      st128(smem + KV_OFF_V + (srow + 32 * i) * LD + scol, gload16(v + g));
     }
   }
 
-  // Staging of one query step (Q and dO rows, lse * log2e and delta) through registers.
-  const int s_tensor = tid / (NT / 2);              // threads [0, NT/2): Q, the rest: dO
-  const int s_unit = tid % (NT / 2);
-  const int s_row = s_unit >> 4, s_col = 8 * (s_unit & 15);
-  constexpr int SROWS = (NT / 2) / 16;              // rows covered per staging pass
-  u32x4 sreg[SPT];
-  float st_lse = 0.f, st_del = 0.f;
-  auto gload_step = [&](int h, int qs0) {
-    const uint16_t* base = (s_tensor ? dout : q) + h * D + s_col;
+  const int n_steps = (doc_end - k0 + BQ - 1) / BQ;
+  const int n_pairs = (n_steps + 1) / 2;
+
+  // Staging of a step pair: thread chunk i is (step half i >> 1, tensor i & 1 = Q / dO), row
+  // tid >> 4, 16-byte column tid & 15. The dO chunk's row dot product with O gives delta.
+  const int s_row = tid >> 4, s_col = 8 * (tid & 15);
+  u32x4 sreg[4];
+  float dpart[2];
+  float st_lse = 0.f;
+  auto gload_pair = [&](int p) {
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) {
-      const long row = min(qs0 + s_row + SROWS * i, doc_end - 1);
-      sreg[i] = gload16(base + row * qrow);
+    for (int i = 0; i < 4; ++i) {
+      const int qs0 = k0 + min(2 * p + (i >> 1), n_steps - 1) * BQ;
+      const long row = min(qs0 + s_row, doc_end - 1);
+      const long g = row * qrow + h * D + s_col;
+      sreg[i] = gload16(((i & 1) ? dout : q) + g);
+      if (i & 1) {
+        const u32x4 o8 = gload16(out + g);
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          acc += E::to_f32(half_of(o8, e)) * E::to_f32(half_of(sreg[i], e));
+        dpart[i >> 1] = acc;
+      }
     }
-    if (tid < BQ) {
-      const int row = qs0 + tid;
-      const bool ok = row < doc_end;
-      st_lse = ok ? lse[(long)h * n_tokens + row] * kLog2e : INFINITY;
-      st_del = ok ? delta[(long)h * n_tokens + row] : 0.f;
+    if (tid < 64) {
+      const int row = k0 + min(2 * p + (tid >> 5), n_steps - 1) * BQ + (tid & 31);
+      st_lse = row < doc_end ? lse[(long)h * n_tokens + row] * kLog2e : INFINITY;
     }
   };
-  auto store_step = [&](int stage) {
-    lds_u16* base = smem + (s_tensor ? OFF_DO : OFF_Q) + stage * QTILE + s_row * LD + s_col;
+  auto store_pair = [&](int stage) {
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) st128(base + SROWS * i * LD, sreg[i]);
-    if (tid < BQ) {
-      stat_raw[stage][0][tid] = st_lse;
-      stat_raw[stage][1][tid] = st_del;
+    for (int i = 0; i < 4; ++i)
+      st128(smem + ((i & 1) ? KV_OFF_DO : KV_OFF_Q) + (stage * 2 + (i >> 1)) * ROWT +
+                s_row * LD + s_col,
+            sreg[i]);
+#pragma unroll
+    for (int sh = 0; sh < 2; ++sh) {  // delta: sum over the 16 threads that share a row
+      float d = dpart[sh];
+      d += __shfl_xor(d, 8, 16);
+      d += __shfl_xor(d, 4, 16);
+      d += __shfl_xor(d, 2, 16);
+      d += __shfl_xor(d, 1, 16);
+      if ((tid & 15) == 0) stat[stage][sh][1][s_row] = d;
     }
+    if (tid < 64) stat[stage][tid >> 5][0][tid & 31] = st_lse;
   };
 
-  // Per-lane LDS read bases (halfs).
-  const int rm_read = perm32(l32) * LD + 8 * hi;                              // rows = queries
+  const int rm_read = perm32(l32) * LD + 8 * hi;                 // A rows = queries
+  const int kv_read = (32 * strip + l32) * LD + 8 * hi;          // B columns = keys
   const int tr_read = (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) + 4 * (src & 3);
-  const int dst_read = OFF_DST + (8 * hi + 2 * (src >> 2)) * LDT + 16 * (grp & 1) + 4 * (src & 3);
-  const int dst_write = OFF_DST + (32 * wave + l32) * LDT + 8 * hi;
 
   f32x16 dkacc[4], dvacc[4];
 #pragma unroll
@@ -173,187 +135,321 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     dvacc[db] = f32x16{};
   }
 
-  // The (head, query step) sequence of this work item.
-  const int steps_per_head = (doc_end - k0 + BQ - 1) / BQ;
-  const int n_steps = steps_per_head * h_count;
-  auto step_head = [&](int s) { return h_begin + s / steps_per_head; };
-  auto step_q0 = [&](int s) { return k0 + (s % steps_per_head) * BQ; };
-
-  gload_step(step_head(0), step_q0(0));
-  store_step(0);
-  if (n_steps > 1) gload_step(step_head(1), step_q0(1));
+  gload_pair(0);
+  store_pair(0);
   __syncthreads();
-
-  for (int s = 0; s < n_steps; ++s) {
-    const int stage = s & 1;
-    const int h = step_head(s), qs0 = step_q0(s);
-    const lds_u16* qs = smem + OFF_Q + stage * QTILE;
-    const lds_u16* dos = smem + OFF_DO + stage * QTILE;
-
-    // S = Q K^T and dP = dO V^T (rows = queries, columns = this wave's keys).
-    f32x16 sacc = f32x16{}, pacc = f32x16{};
+  for (int p = 0; p < n_pairs; ++p) {
+    const int stage = p & 1;
+    if (p + 1 < n_pairs) gload_pair(p + 1);
+    const int s = 2 * p + half;
+    const int qs0 = k0 + s * BQ;
+    if (s < n_steps && kw0 <= qs0 + BQ - 1) {
+      const lds_u16* qs = smem + KV_OFF_Q + (stage * 2 + half) * ROWT;
+      const lds_u16* dos = smem + KV_OFF_DO + (stage * 2 + half) * ROWT;
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      sacc = E::mfma(ld128(qs + rm_read + 16 * kk), kf[kk], sacc);
-      pacc = E::mfma(ld128(dos + rm_read + 16 * kk), vf[kk], pacc);
-    }
-    // register j <-> query qs0 + reg_row(j, hi) = qs0 + 16 (j >> 3) + 8 hi + (j & 7).
-    float p[16], ds[16];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int r0 = 16 * c + 8 * hi;
-      const lds_f32x4* st = reinterpret_cast<const lds_f32x4*>(
-          (__attribute__((address_space(3))) float*)&stat_raw[stage][0][0]);
-      const f32x4 l0 = st[r0 / 4], l1 = st[r0 / 4 + 1];
-      const f32x4 d0 = st[(BQ + r0) / 4], d1 = st[(BQ + r0) / 4 + 1];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int j = 8 * c + e;
-        const float lv = e < 4 ? l0[e] : l1[e - 4];
-        p[j] = fast_exp2(fmaf(sacc[j], scale_log2, -lv));
-        ds[j] = e < 4 ? d0[e] : d1[e - 4];
+      for (int kk = 0; kk < 8; ++kk) {
+        sacc = E::mfma(ld128(qs + rm_read + 16 * kk), ld128(smem + KV_OFF_K + kv_read + 16 * kk),
+                       sacc);
+        pacc = E::mfma(ld128(dos + rm_read + 16 * kk), ld128(smem + KV_OFF_V + kv_read + 16 * kk),
+                       pacc);
       }
-    }
-    if (kw0 + 31 > qs0) {  // the step crosses this wave's diagonal: key > query -> P = 0
+      // register j <-> query qs0 + reg_row(j, hi); P overwrites S, dS overwrites dP.
+      const lds_f32x4* st = reinterpret_cast<const lds_f32x4*>(
+          (__attribute__((address_space(3))) float*)&stat[stage][half][0][0]);
+      const bool diag = kw0 + 31 > qs0;
       const int lim = my_key - qs0;
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (reg_row(j, hi) < lim) p[j] = 0.f;
-    }
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ds[j] = p[j] * (pacc[j] - ds[j]);
-
-    // dV += P^T dO and dK += dS^T Q: A = this lane's key row (k = queries), B via tr reads.
+        for (int g4 = 0; g4 < 2; ++g4) {
+          const int r0 = 16 * c + 8 * hi + 4 * g4;
+          const f32x4 l4 = st[r0 / 4];
+          const f32x4 d4 = st[(BQ + r0) / 4];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const u32x4 pa = pack8_tr<E>(p + 8 * c);
-      const u32x4 da = pack8_tr<E>(ds + 8 * c);
+          for (int e = 0; e < 4; ++e) {
+            const int j = 8 * c + 4 * g4 + e;
+            float pv = fast_exp2(fmaf(sacc[j], scale_log2, -l4[e]));
+            if (diag && reg_row(j, hi) < lim) pv = 0.f;  // key > query
+            sacc[j] = pv;
+            pacc[j] = pv * (pacc[j] - d4[e]);
+          }
+        }
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int off = tr_read + 16 * c * LD + 32 * db;
-        dvacc[db] = E::mfma(pa, ldtr8(dos + off, LD), dvacc[db]);
-        dkacc[db] = E::mfma(da, ldtr8(qs + off, LD), dkacc[db]);
-      }
-    }
-    // dS^T rows (this lane's key), queries in natural order.
+      for (int c = 0; c < 2; ++c) {
+        float pv8[8], dv8[8];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int j0 = 8 * c;
-      st128(smem + dst_write + 16 * c,
-            pack8<E>(ds[j0], ds[j0 + 1], ds[j0 + 2], ds[j0 + 3], ds[j0 + 4], ds[j0 + 5],
-                     ds[j0 + 6], ds[j0 + 7]));
-    }
-    // Next step's Q/dO into the other stage (its readers finished before the last barrier).
-    if (s + 1 < n_steps) {
-      store_step(stage ^ 1);
-      if (s + 2 < n_steps) gload_step(step_head(s + 2), step_q0(s + 2));
-    }
-    __syncthreads();
-
-    // dQ rows [qs0, qs0 + 32), columns [32 w, 32 w + 32) = dS (32 x BN) K (BN x 32).
-    {
-      f32x16 acc = f32x16{};
+        for (int e = 0; e < 8; ++e) {
+          pv8[e] = sacc[8 * c + e];
+          dv8[e] = pacc[8 * c + e];
+        }
+        const u32x4 pa = pack8_tr<E>(pv8);
+        const u32x4 da = pack8_tr<E>(dv8);
 #pragma unroll
-      for (int kc = 0; kc < BN / 16; ++kc) {
-        const u32x4 a = ldtr8(smem + dst_read + 16 * kc * LDT, LDT);
-        const u32x4 b = ldtr8(smem + OFF_K + tr_read + 16 * kc * LD + 32 * wave, LD);
-        acc = E::mfma(a, b, acc);
-      }
-      // register j <-> query qs0 + 8 (j >> 2) + 4 hi + (j & 3), column 32 w + l32.
-      float* dqp = dq_acc + (long)qs0 * qrow + (long)h * D + 32 * wave + l32;
-      const int rows_left = doc_end - qs0;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = 8 * (j >> 2) + 4 * hi + (j & 3);
-        if (r < rows_left) atomicAdd(dqp + (long)r * qrow, acc[j] * scale);
-      }
-    }
-    __syncthreads();
-  }
-
-  // dK, dV of this wave's keys: register j <-> key kw0 + 8 (j >> 2) + 4 hi + (j & 3), column
-  // d = 32 db + l32.
-  if (kw0 < doc_end) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = kw0 + 8 * (j >> 2) + 4 * hi + (j & 3);
-        if (key < doc_end) {
-          const long off = ((long)key * hkv + kvh) * D + 32 * db + l32;
-          atomicAdd(dk_acc + off, dkacc[db][j] * scale);
-          atomicAdd(dv_acc + off, dvacc[db][j]);
+        for (int db = 0; db < 4; ++db) {
+          const int off = tr_read + 16 * c * LD + 32 * db;
+          dvacc[db] = E::mfma(pa, ldtr8(dos + off, LD), dvacc[db]);
+          dkacc[db] = E::mfma(da, ldtr8(qs + off, LD), dkacc[db]);
         }
       }
     }
+    if (p + 1 < n_pairs) store_pair(stage ^ 1);
+    __syncthreads();
+  }
+
+  // Half 1 hands its partial sums to half 0 (same lane order), which writes this head's dK/dV.
+  float* xk = reinterpret_cast<float*>((uint16_t*)smem);
+  if (half == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        xk[(strip * 128 + 16 * db + j) * 64 + lane] = dkacc[db][j];
+        xk[(strip * 128 + 64 + 16 * db + j) * 64 + lane] = dvacc[db][j];
+      }
+  }
+  __syncthreads();
+  if (half == 1 || kw0 >= doc_end) return;
+  // register j <-> key kw0 + 8 (j >> 2) + 4 hi + (j & 3), column d = 32 db + l32.
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int key = kw0 + 8 * (j >> 2) + 4 * hi + (j & 3);
+    if (key < doc_end) {
+      uint16_t* dkp = dk_part + ((long)key * hq + h) * D + l32;
+      uint16_t* dvp = dv_part + ((long)key * hq + h) * D + l32;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const float dkv = dkacc[db][j] + xk[(strip * 128 + 16 * db + j) * 64 + lane];
+        const float dvv = dvacc[db][j] + xk[(strip * 128 + 64 + 16 * db + j) * 64 + lane];
+        dkp[32 * db] = E::from_f32(dkv * scale);
+        dvp[32 * db] = E::from_f32(dvv);
+      }
+    }
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// fp32 accumulators -> element type, 8 elements per thread.
-// ---------------------------------------------------------------------------------------------
+// --------------------------------------------------------------------------------------------
+// q item: dQ of 128 queries for one query head.
+// --------------------------------------------------------------------------------------------
 template <class E>
-__global__ __launch_bounds__(256) void bwd_post_kernel(const float* __restrict__ src,
-                                                       uint16_t* __restrict__ dst, long n8) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n8) return;
-  const f32x4 a = reinterpret_cast<const f32x4*>(src)[2 * i];
-  const f32x4 b = reinterpret_cast<const f32x4*>(src)[2 * i + 1];
-  gstore16(dst + 8 * i, pack8<E>(a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]));
+__device__ __forceinline__ void bwd_q_item(
+    lds_u16* smem, const int4 it, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
+    const float* __restrict__ lse, uint16_t* __restrict__ dq, int n_tokens, int hq, int hkv,
+    float scale, float scale_log2) {
+  using namespace bwd;
+  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & 0xffffff;
+  const int kvh = h / (hq / hkv);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int half = wave / NS, strip = wave % NS;
+  const int src = lane & 15, grp = lane >> 4;
+  const long qrow = (long)hq * D, kvrow = (long)hkv * D;
+  const int wq0 = q0 + 32 * strip;
+  const int my_q = wq0 + l32;
+  const bool q_valid = my_q < doc_end;
+
+  // Q and dO rows of this lane's query as B operands (k slots = d); lse and delta in-lane.
+  u32x4 qf[8], df[8];
+  float lse2, dlt;
+  {
+    const long g = (long)min(my_q, doc_end - 1) * qrow + h * D + 8 * hi;
+    float acc = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      qf[kk] = gload16(q + g + 16 * kk);
+      df[kk] = gload16(dout + g + 16 * kk);
+      const u32x4 o8 = gload16(out + g + 16 * kk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += E::to_f32(half_of(o8, e)) * E::to_f32(half_of(df[kk], e));
+    }
+    dlt = sum_with_other_half(acc);
+    lse2 = q_valid ? lse[(long)h * n_tokens + my_q] * kLog2e : INFINITY;
+  }
+
+  const int kv_end = min(q0 + QB, doc_end);
+  const int n_tiles = (kv_end - doc_start + BT - 1) / BT;
+  const int n_pairs = (n_tiles + 1) / 2;
+
+  // Staging of a tile pair: chunk i is (tile i >> 1, tensor i & 1 = K / V), row tid >> 4.
+  const int srow = tid >> 4, scol = 8 * (tid & 15);
+  u32x4 sr[4];
+  auto gload_pair = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const long row = min(doc_start + (2 * p + (i >> 1)) * BT + srow, doc_end - 1);
+      sr[i] = gload16(((i & 1) ? v : k) + row * kvrow + kvh * D + scol);
+    }
+  };
+  auto store_pair = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st128(smem + stage * Q_PAIR + i * ROWT + srow * LD + scol, sr[i]);
+  };
+
+  // LDS read bases: K / V rows as A operands (rows = keys through perm32, k = d); K^T through
+  // transposed reads with the column order that keeps output registers d-contiguous.
+  const int ka_read = (2 * half) * ROWT + perm32(l32) * LD + 8 * hi;
+  const int va_read = (2 * half + 1) * ROWT + perm32(l32) * LD + 8 * hi;
+  const int kt_read = (2 * half) * ROWT + (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) +
+                      4 * ((((src & 3) & 1) << 1) | ((src & 3) >> 1));
+
+  f32x16 dqacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) dqacc[db] = f32x16{};
+
+  gload_pair(0);
+  store_pair(0);
+  __syncthreads();
+  for (int p = 0; p < n_pairs; ++p) {
+    const int stage = p & 1;
+    if (p + 1 < n_pairs) gload_pair(p + 1);
+    const int t = 2 * p + half;
+    const int kv0 = doc_start + t * BT;
+    if (t < n_tiles && kv0 <= wq0 + 31) {
+      const lds_u16* base = smem + stage * Q_PAIR;
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        sacc = E::mfma(ld128(base + ka_read + 16 * kk), qf[kk], sacc);
+        pacc = E::mfma(ld128(base + va_read + 16 * kk), df[kk], pacc);
+      }
+      // register j <-> key kv0 + reg_row(j, hi), query my_q.
+      const bool diag = kv0 + 31 > wq0;
+      const int lim = my_q - kv0;
+      float ds[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float pv = fast_exp2(fmaf(sacc[j], scale_log2, -lse2));
+        if (diag && reg_row(j, hi) > lim) pv = 0.f;  // key > query
+        ds[j] = pv * (pacc[j] - dlt);
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x4 bf = pack8_tr<E>(ds + 8 * c);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          dqacc[db] = E::mfma(ldtr8(base + kt_read + 16 * c * LD + 32 * db, LD), bf, dqacc[db]);
+      }
+    }
+    if (p + 1 < n_pairs) store_pair(stage ^ 1);
+    __syncthreads();
+  }
+
+  // Half 1 hands its partial dQ^T to half 0 (same lane order), which scales and writes it.
+  float* xq = reinterpret_cast<float*>((uint16_t*)smem);
+  if (half == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xq[(strip * 64 + 16 * db + j) * 64 + lane] = dqacc[db][j];
+  }
+  __syncthreads();
+  if (half == 1 || !q_valid) return;
+  uint16_t* dqp = dq + (long)my_q * qrow + h * D;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      x[j] = (dqacc[db][j] + xq[(strip * 64 + 16 * db + j) * 64 + lane]) * scale;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int j0 = 8 * c;  // register j <-> d = 32 db + reg_row(j, hi)
+      gstore16(dqp + 32 * db + 16 * c + 8 * hi,
+               pack8<E>(x[j0], x[j0 + 1], x[j0 + 2], x[j0 + 3], x[j0 + 4], x[j0 + 5], x[j0 + 6],
+                        x[j0 + 7]));
+    }
+  }
 }
 
 template <class E>
-static hipError_t launch_bwd_prepare_t(const BwdArgs& a) {
-  const long rows = a.n_tokens * a.hq;
-  if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(bwd_pre_kernel<E>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
-                     a.stream, (const uint16_t*)a.out, (const uint16_t*)a.dout, a.delta,
-                     a.dq_acc, a.dk_acc, a.dv_acc, (int)a.n_tokens, a.hq, a.hkv);
-  return hipGetLastError();
+__global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ out,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse, uint16_t* __restrict__ dq,
+    uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part,
+    const int4* __restrict__ items, int n_tokens, int hq, int hkv, float scale,
+    float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
+  __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][half][lse|del]
+  lds_u16* smem = (lds_u16*)smem_raw;
+  const int4 it = items[blockIdx.x];
+  if ((it.w >> 24) == bwd::kKindKV) {
+    bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,
+                   scale, scale_log2);
+  } else {
+    bwd_q_item<E>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale, scale_log2);
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// dK/dV = sum over the G query heads of each key/value head of the per-head partials (fp32 sum
+// of the 16-bit partials, one rounding); 8 elements per thread.
+// --------------------------------------------------------------------------------------------
+template <class E>
+__global__ __launch_bounds__(256) void bwd_gqa_sum_kernel(const uint16_t* __restrict__ dk_part,
+                                                          const uint16_t* __restrict__ dv_part,
+                                                          uint16_t* __restrict__ dk,
+                                                          uint16_t* __restrict__ dv, long n8,
+                                                          int hq, int hkv) {
+  long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const uint16_t* src = dk_part;
+  uint16_t* dst = dk;
+  if (i >= n8) {
+    i -= n8;
+    src = dv_part;
+    dst = dv;
+    if (i >= n8) return;
+  }
+  // i indexes 8-element chunks of (N, Hkv, D): row r = token * Hkv + kvh, chunk c of 16.
+  const long r = i >> 4;
+  const int c = (int)(i & 15);
+  const long token = r / hkv;
+  const int kvh = (int)(r - token * hkv);
+  const int g = hq / hkv;
+  const uint16_t* p = src + (token * hq + (long)kvh * g) * kHeadDim + 8 * c;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int x = 0; x < g; ++x) {
+    const u32x4 w = gload16(p + x * kHeadDim);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += E::to_f32(half_of(w, e));
+  }
+  gstore16(dst + 8 * i, pack8<E>(acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], acc[6], acc[7]));
 }
 
 template <class E>
 static hipError_t launch_bwd_main_t(const BwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
-  hipLaunchKernelGGL((bwd_kernel<E>), dim3((unsigned)a.n_items), dim3(bwd::NT),
-                     0, a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
-                     (const uint16_t*)a.v, (const uint16_t*)a.dout, a.lse, a.delta, a.dq_acc,
-                     a.dk_acc, a.dv_acc, (const int4*)a.items, (int)a.n_tokens, a.hq, a.hkv,
-                     a.scale, a.scale * kLog2e);
+  hipLaunchKernelGGL((bwd_kernel<E>), dim3((unsigned)a.n_items), dim3(bwd::NT), 0, a.stream,
+                     (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
+                     (const uint16_t*)a.out, (const uint16_t*)a.dout, a.lse, (uint16_t*)a.dq,
+                     (uint16_t*)a.dk_part, (uint16_t*)a.dv_part, (const int4*)a.items,
+                     (int)a.n_tokens, a.hq, a.hkv, a.scale, a.scale * kLog2e);
   return hipGetLastError();
 }
 
 template <class E>
 static hipError_t launch_bwd_finish_t(const BwdArgs& a) {
-  const struct {
-    const float* src;
-    void* dst;
-    long n;
-  } outs[3] = {{a.dq_acc, a.dq, a.n_tokens * a.hq * kHeadDim},
-               {a.dk_acc, a.dk, a.n_tokens * a.hkv * kHeadDim},
-               {a.dv_acc, a.dv, a.n_tokens * a.hkv * kHeadDim}};
-  for (const auto& t : outs) {
-    if (t.dst == nullptr || t.n == 0) continue;
-    const long n8 = t.n / 8;
-    hipLaunchKernelGGL(bwd_post_kernel<E>, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0,
-                       a.stream, t.src, (uint16_t*)t.dst, n8);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  return hipSuccess;
+  if (a.dk == nullptr || a.dk_part == a.dk) return hipSuccess;  // partials are the result
+  const long n8 = a.n_tokens * a.hkv * kHeadDim / 8;
+  if (n8 == 0) return hipSuccess;
+  hipLaunchKernelGGL(bwd_gqa_sum_kernel<E>, dim3((unsigned)((2 * n8 + 255) / 256)), dim3(256), 0,
+                     a.stream, (const uint16_t*)a.dk_part, (const uint16_t*)a.dv_part,
+                     (uint16_t*)a.dk, (uint16_t*)a.dv, n8, a.hq, a.hkv);
+  return hipGetLastError();
 }
 
 hipError_t launch_bwd_stage(const BwdArgs& a, int stage) {
   const bool bf = a.dtype != 0;
   switch (stage) {
-    case 0: return bf ? launch_bwd_prepare_t<BF16>(a) : launch_bwd_prepare_t<F16>(a);
+    case 0: return hipSuccess;  // nothing to prepare: delta is computed inside the main kernel
     case 1: return bf ? launch_bwd_main_t<BF16>(a) : launch_bwd_main_t<F16>(a);
     default: return bf ? launch_bwd_finish_t<BF16>(a) : launch_bwd_finish_t<F16>(a);
   }
 }
 
 hipError_t launch_bwd(const BwdArgs& a) {
-  for (int stage = 0; stage < 3; ++stage) {
+  for (int stage = 1; stage < 3; ++stage) {
     hipError_t e = launch_bwd_stage(a, stage);
     if (e != hipSuccess) return e;
   }

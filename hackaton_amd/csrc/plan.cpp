@@ -49,9 +49,18 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
         for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, h, work});
       }
     } else {
+      // kv items: the two halves take alternate 32-query steps over the 128 keys
       for (int32_t k0 = s; k0 < e; k0 += va::kBwdBlockN) {
-        const int64_t work = e - k0;  // queries visited by the tile
-        for (int32_t h = 0; h < hq; ++h) items.push_back({k0, e, h, 1, work});
+        const int64_t steps = ((int64_t)e - k0 + va::kBwdBlockQ - 1) / va::kBwdBlockQ;
+        const int64_t work = (steps + 1) / 2 * 32;  // MFMAs per wave per step pair
+        for (int32_t h = 0; h < hq; ++h) items.push_back({k0, e, s, h, work});
+      }
+      // q items: the two halves take alternate 32-key tiles up to the diagonal
+      for (int32_t q0 = s; q0 < e; q0 += va::kBwdBlockM) {
+        const int64_t kv_end = std::min<int64_t>((int64_t)q0 + va::kBwdBlockM, e);
+        const int64_t tiles = (kv_end - s + va::kBwdTileK - 1) / va::kBwdTileK;
+        const int64_t work = (tiles + 1) / 2 * 24;
+        for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, (1 << 24) | h, work});
       }
     }
   }
@@ -62,10 +71,15 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
 
 int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
   int64_t n = 0;
-  const int64_t tile = kind == VA_PLAN_FWD ? va::kFwdBlockM : va::kBwdBlockN;
   for (int32_t i = 0; i < n_docs; ++i) {
     const int64_t len = (int64_t)cu[i + 1] - cu[i];
-    if (len > 0) n += (len + tile - 1) / tile * hq;
+    if (len <= 0) continue;
+    if (kind == VA_PLAN_FWD) {
+      n += (len + va::kFwdBlockM - 1) / va::kFwdBlockM * hq;
+    } else {
+      n += (len + va::kBwdBlockN - 1) / va::kBwdBlockN * hq;
+      n += (len + va::kBwdBlockM - 1) / va::kBwdBlockM * hq;
+    }
   }
   return n;
 }

@@ -11,9 +11,10 @@ constexpr int kHeadDim = 128;  // Qwen2.5-1.5B / 7B head size; the kernels are b
 // Tile geometry; the plan builder (plan.cpp) emits work items for exactly these shapes.
 constexpr int kFwdWaves = 4;                 // forward: 32 queries per wave
 constexpr int kFwdBlockM = 32 * kFwdWaves;   // queries per forward work item
-constexpr int kBwdWaves = 4;                 // backward: 32 keys per wave
-constexpr int kBwdBlockN = 32 * kBwdWaves;   // keys per backward work item
-constexpr int kBwdBlockQ = 32;               // queries per backward inner step
+constexpr int kBwdBlockN = 128;  // keys per backward kv work item
+constexpr int kBwdBlockQ = 32;   // queries per kv-item step
+constexpr int kBwdBlockM = 128;  // queries per backward q work item
+constexpr int kBwdTileK = 32;    // keys per q-item tile
 
 struct FwdArgs {
   const void* q;
@@ -37,18 +38,17 @@ struct BwdArgs {
   const void* v;
   const void* out;
   const float* lse;
-  const int32_t* items;  // int4 per work item: {k0, doc_end, head_begin, head_count}
+  const int32_t* items;  // int4 per work item: kv {k0, doc_end, -, head}, q {q0, doc_end,
+                         // doc_start, (1 << 24) | head}
   int64_t n_items;
   int64_t n_tokens;
   int hq, hkv;
   float scale;
   int dtype;
-  float* delta;    // (hq, n_tokens)
-  float* dq_acc;   // (n_tokens, hq, 128)
-  float* dk_acc;   // (n_tokens, hkv, 128)
-  float* dv_acc;   // (n_tokens, hkv, 128)
-  void* dq;        // outputs in the element type, or null to keep the fp32 accumulators only
-  void* dk;
+  void* dq;         // (n_tokens, hq, 128), written by the q items
+  void* dk_part;    // (n_tokens, hq, 128) per-query-head dK (== dk when hq == hkv)
+  void* dv_part;
+  void* dk;         // (n_tokens, hkv, 128) GQA sums, or null to keep the per-head partials
   void* dv;
   hipStream_t stream;
 };

@@ -10,7 +10,7 @@
  * Layouts (row-major, contiguous, 16-byte aligned):
  *   q, out, dq      (N, Hq, 128)   16-bit (dtype VA_F16 or VA_BF16)
  *   k, v, dk, dv    (N, Hkv, 128)  16-bit; GQA: query head h reads key/value head h / (Hq/Hkv)
- *   lse, delta      (Hq, N)        fp32, natural-log log-sum-exp of each query row
+ *   lse             (Hq, N)        fp32, natural-log log-sum-exp of each query row
  *   cu_seqlens      (n_docs + 1)   int32 host array, cu[0] = 0, non-decreasing; document i is
  *                                  rows [cu[i], cu[i+1]) of the packed token axis
  *   work items      int32 x 4 each, built on the host by va_plan_build and copied to the device
@@ -57,8 +57,8 @@ int32_t va_head_dim(void);
 
 /* ---- work plan (host only; no GPU call) ------------------------------------------------------
  * Work items for the forward (kind VA_PLAN_FWD: one per 128-query tile x query head) or the
- * backward (VA_PLAN_BWD: one per 128-key tile x query head) over the documents of cu_seqlens,
- * ordered longest first. Fully masked causal tiles and cross-document tiles never appear.
+ * backward (VA_PLAN_BWD: one per 128-key tile x query head for dK/dV and one per 128-query tile
+ * x query head for dQ) over the documents of cu_seqlens, ordered longest first. Fully masked causal tiles and cross-document tiles never appear.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
 int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                  int64_t* n_items);
@@ -74,21 +74,24 @@ int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
            int32_t head_dim, float scale, int32_t dtype, void* stream);
 
 /* ---- attention backward -----------------------------------------------------------------------
- * Workspace: delta (Hq, N) fp32 and fp32 accumulators dq (N, Hq, 128), dk, dv (N, Hkv, 128),
- * at the byte offsets va_bwd_workspace_layout reports. dq/dk/dv may be NULL: the fp32
- * accumulators in the workspace are then the result (read them at the reported offsets).
+ * Deterministic and atomic-free. dq (N, Hq, 128) is always written. dk/dv (N, Hkv, 128) are the
+ * sums over each GQA group of per-query-head partials (N, Hq, 128, element type) that live in the
+ * workspace at the offsets va_bwd_workspace_layout reports; with dk = dv = NULL the partials are
+ * the result (a rotary backward can sum them, as the reference sums its expanded copies). With
+ * Hq == Hkv and dk/dv given, no workspace is used. The caller's O and lse come from va_fwd;
+ * rowsum(dO * O) is computed inside.
  * Replaces: solution/attention.py:230-232 (aten::_efficient_attention_backward) and the GQA
  * reduction of dk/dv at solution/attention.py:113-134. */
 int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim,
-                            int64_t offsets[4], int64_t* bytes);
+                            int64_t offsets[2], int64_t* bytes);
 int va_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,
            const float* lse, const int32_t* items, int64_t n_items, int64_t total_tokens,
            int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype, void* dq,
            void* dk, void* dv, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* The same backward in its three launches, for callers that time or overlap them separately:
- * prepare (delta = rowsum(dO * O), clears the accumulators), main (dQ/dK/dV accumulation), finish
- * (casts the accumulators to dq/dk/dv; nothing when they are NULL). Same arguments as va_bwd.
+/* The same backward in its stages, for callers that time or overlap them separately: prepare
+ * (nothing to do in this implementation), main (dQ and the per-head dK/dV partials), finish (the
+ * GQA sums into dk/dv; nothing when they are NULL or Hq == Hkv). Same arguments as va_bwd.
  * Replaces: the same reference call as va_bwd (solution/attention.py:230-232). */
 int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k, const void* v,
                  const void* out, const float* lse, const int32_t* items, int64_t n_items,

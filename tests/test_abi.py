@@ -57,18 +57,22 @@ def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
 
 
 @pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1], [257, 3]])
-def test_backward_plan_covers_every_key_tile_once(lengths):
+def test_backward_plan_covers_every_key_and_query_tile_once(lengths):
+    """kv items (dK/dV of 128 keys) and q items (dQ of 128 queries), one per head each."""
     hq, hkv = 12, 2
     cu, items = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
-    seen = set()
-    for k0, doc_end, h0, count in items.tolist():
-        assert count == 1 and 0 <= h0 < hq
-        d = int(np.searchsorted(cu, k0, side="right")) - 1
-        assert cu[d + 1] == doc_end and (k0 - cu[d]) % 128 == 0
-        seen.add((k0, h0))
-    expected = {(k0, h) for s, e in zip(cu[:-1], cu[1:]) for k0 in range(s, e, 128)
+    kv_seen, q_seen = set(), set()
+    for a, doc_end, doc_start, w in items.tolist():
+        kind, h = w >> 24, w & 0xffffff
+        assert 0 <= h < hq and kind in (0, 1)
+        d = int(np.searchsorted(cu, doc_start, side="right")) - 1
+        assert cu[d] == doc_start and cu[d + 1] == doc_end
+        assert doc_start <= a < doc_end and (a - doc_start) % 128 == 0
+        (kv_seen if kind == 0 else q_seen).add((a, h))
+    expected = {(t, h) for s, e in zip(cu[:-1], cu[1:]) for t in range(s, e, 128)
                 for h in range(hq)}
-    assert seen == expected and len(items) == len(expected)
+    assert kv_seen == expected and q_seen == expected
+    assert len(items) == 2 * len(expected)
 
 
 def test_plan_rejects_bad_cu_seqlens():
@@ -113,15 +117,17 @@ def test_attention_entry_points_validate_before_launching():
     assert rc == _lib.VA_EINVAL and b"positive" in lib.va_last_error()
     # nothing to do is not an error
     assert lib.va_fwd(None, None, None, None, None, None, 0, 0, 12, 2, 128, 0.1, 0, None) == 0
-    offs = (ctypes.c_int64 * 4)()
+    offs = (ctypes.c_int64 * 2)()
     nbytes = ctypes.c_int64()
     assert lib.va_bwd_workspace_layout(2048, 12, 2, 128, offs, ctypes.byref(nbytes)) == 0
-    assert list(offs) == [0, 98304, 98304 + 2048 * 12 * 512, 98304 + 2048 * 12 * 512
-                          + 2048 * 2 * 512]
-    assert nbytes.value == offs[3] + 2048 * 2 * 512
-    rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, None,
+    assert list(offs) == [0, 2048 * 12 * 256]
+    assert nbytes.value == 2 * 2048 * 12 * 256
+    rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, fake,
                     None, None, fake, nbytes.value - 1, None)
     assert rc == _lib.VA_ECAPACITY
+    rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, fake,
+                    fake, None, fake, nbytes.value, None)
+    assert rc == _lib.VA_EINVAL and b"both" in lib.va_last_error()
     rc = lib.va_rope_fwd(fake, fake, fake, fake, fake, 0, 128, fake, fake, fake, fake, fake, 10,
                          12, 2, 128, 0, 0, 0, 1, 0, None)
     assert rc == _lib.VA_EINVAL  # padded layout needs seq > 0
