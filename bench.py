@@ -8,10 +8,12 @@ resident buffer sets, launched as one captured HIP graph. Inputs are N(0, 1), sy
 Metric: causal-FLOP throughput, F = 3.5 * 4 * Hq * D * sum L(L+1)/2 per call (forward + backward,
 the backward's recomputation of P not counted), in TFLOP/s and as a fraction of the MI355X dense
 fp16 MFMA peak. The dominant kernel's duration is measured with HIP events on the stream it runs
-on (queue pre-filled so launch latency is not timed) and reported against its roofline. The CPU
-baseline is the oracle (numpy fp32) on one layer call of the same shape, on this host's cores.
+on (each kernel captured alone, 28 launches per graph replay) and reported against its roofline,
+with the HBM traffic that rocprofv3 --pmc measured for it (profiles/hbm_traffic_<workload>.md). The
+CPU baseline is the oracle (numpy fp32) on one layer call of the same shape, on this host's cores.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config 2]
+    python bench.py --pmc-probe          # untimed launches for rocprofv3 --pmc passes
 """
 
 import argparse
@@ -38,6 +40,9 @@ def parse():
     p.add_argument("--config", type=int, default=2)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--pmc-probe", action="store_true",
+                   help="launch a 256 MiB fp32 copy-like kernel and each attention kernel once per "
+                        "buffer set, untimed, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     return p.parse_args()
 
 
@@ -60,6 +65,21 @@ class LayerSet:
         self.ws, _ = att.bwd_workspace(n, hq, hkv, dev)
         self.n, self.hq, self.hkv = n, hq, hkv
         self.plan = plan
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` as measured by rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE (each scaled by the same counter's reading on a copy kernel of known size), read from
+    the committed profile summary; None when no measurement is committed."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch:" and parts[1] == kernel:
+                return int(parts[2])
+    return None
 
 
 def main():
@@ -113,6 +133,26 @@ def main():
             fwd(s, stream)
             bwd(s, stream)
 
+    if args.pmc_probe:
+        # calibration kernel of known traffic: y = x * 1 over 64 Mi fp32 (256 MiB read, 256 MiB
+        # written), then every attention kernel once per buffer set
+        x = torch.randn(64 << 20, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.mul(x, 1.0, out=y)
+        stream = torch.cuda.current_stream().cuda_stream
+        for s in sets:
+            fwd(s, stream)
+        for s in sets:
+            bwd(s, stream, _lib.VA_BWD_MAIN)
+        for s in sets:
+            bwd(s, stream, _lib.VA_BWD_FINISH)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_probe": cfg["name"], "copy_read_bytes": x.numel() * 4,
+                          "copy_write_bytes": y.numel() * 4, "launches_per_kernel": len(sets)}),
+              flush=True)
+        return
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -140,50 +180,51 @@ def main():
     tflops = flops_step / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_MFMA_TFLOPS[cfg["dtype"]]
 
-    # ---- dominant-kernel timing: HIP events on the launch stream, queue pre-filled -----------
-    def timed(launch, reps=3):
-        stream = torch.cuda.current_stream()
-        evs = []
-        for _ in range(reps):
-            try:
-                torch.cuda._sleep(20_000_000)  # holds the queue while the launches are enqueued
-            except Exception:
-                pass
+    # ---- dominant-kernel timing: HIP events on the launch stream ------------------------------
+    # Each kernel is captured alone, 28 launches back to back (one per buffer set), and the graph
+    # is replayed between two events recorded on the stream the replays run on; the average
+    # launch duration is the elapsed time over the number of launches.
+    def kernel_graph(launch):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            st = torch.cuda.current_stream().cuda_stream
             for s in sets:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                launch(s, stream, a, b)
-                evs.append((a, b))
+                launch(s, st)
+        return g
+
+    def timed(g, reps=10):
+        g.replay()
         torch.cuda.synchronize()
-        times = [a.elapsed_time(b) * 1e3 for a, b in evs]
-        return float(np.mean(times)), float(np.median(times))
-
-    def fwd_launch(s, stream, a, b):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        fwd(s, stream.cuda_stream)
+        for _ in range(reps):
+            g.replay()
         b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (reps * len(sets))
 
-    def bwd_main_launch(s, stream, a, b):
-        a.record()
-        bwd(s, stream.cuda_stream, _lib.VA_BWD_MAIN)
-        b.record()
-        bwd(s, stream.cuda_stream, _lib.VA_BWD_FINISH)
-
-    fwd_us, fwd_med = timed(fwd_launch)
-    bwd_us, bwd_med = timed(bwd_main_launch)
+    g_fwd = kernel_graph(fwd)
+    g_bwd = kernel_graph(lambda s, st: bwd(s, st, _lib.VA_BWD_MAIN))
+    g_fin = kernel_graph(lambda s, st: bwd(s, st, _lib.VA_BWD_FINISH))
+    fwd_us, bwd_us, fin_us = timed(g_fwd), timed(g_bwd), timed(g_fin)
     fwd_flops = wl.forward_flops(lengths, hq)
     bwd_flops = 2.5 * fwd_flops
+    n_tok = sum(lengths)
     kernels = {
-        "fwd_kernel": dict(us=fwd_us, median_us=fwd_med, flops=fwd_flops,
-                           tflops=fwd_flops / (fwd_us * 1e-6) / 1e12),
-        "bwd_kernel": dict(us=bwd_us, median_us=bwd_med, flops=bwd_flops,
-                           tflops=bwd_flops / (bwd_us * 1e-6) / 1e12),
+        "fwd_kernel": dict(us=fwd_us, flops=fwd_flops,
+                           bytes=wl.forward_bytes(n_tok, hq, hkv)),
+        "bwd_kernel": dict(us=bwd_us, flops=bwd_flops,
+                           bytes=wl.backward_main_bytes(n_tok, hq, hkv)),
+        "bwd_gqa_sum_kernel": dict(us=fin_us, flops=0.0,
+                                   bytes=wl.gqa_sum_bytes(n_tok, hq, hkv)),
     }
     dom_name = max(kernels, key=lambda k: kernels[k]["us"])
     dom = kernels[dom_name]
-    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(dom["tflops"], 2),
-                "peak": peak, "unit": "TFLOP/s", "frac": round(dom["tflops"] / peak, 4),
-                "traffic": None, "avg_us": round(dom["us"], 3),
-                "flops_per_launch": dom["flops"]}
+    achieved = dom["flops"] / (dom["us"] * 1e-6) / 1e12
+    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(achieved, 2),
+                "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                "traffic": measured_traffic(dom_name, cfg["name"]), "avg_us": round(dom["us"], 3),
+                "flops_per_launch": dom["flops"], "algorithmic_bytes": dom["bytes"]}
 
     # ---- CPU baseline: the oracle on one layer call of the same shape ------------------------
     cpu = None
@@ -231,6 +272,8 @@ def main():
         "pct_mfma_peak": round(100 * tflops / peak, 3),
         "wall_ms_per_step": round(wall_ms, 5),
         "kernels_us": {k: round(v["us"], 3) for k, v in kernels.items()},
+        "kernels_tflops": {k: round(v["flops"] / (v["us"] * 1e-6) / 1e12, 2)
+                           for k, v in kernels.items() if v["flops"]},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

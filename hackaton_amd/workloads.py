@@ -116,5 +116,18 @@ def algorithmic_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
     return fwd + bwd
 
 
+def backward_main_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
+    """HBM bytes the backward's main kernel must move: reads q, dO, O, k, v, lse; writes dq and the
+    per-query-head dK/dV partials (or dK/dV themselves when Hq == Hkv)."""
+    return n_tokens * (6 * hq * d * elem + 2 * hkv * d * elem + 4 * hq)
+
+
+def gqa_sum_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
+    """HBM bytes of the backward's GQA reduction: reads the dK/dV partials, writes dK/dV."""
+    if hq == hkv:
+        return 0
+    return n_tokens * 2 * (hq + hkv) * d * elem
+
+
 def forward_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
     return n_tokens * ((hq + 2 * hkv) * d * elem + hq * d * elem + 4 * hq)
