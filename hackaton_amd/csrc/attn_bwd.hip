@@ -80,30 +80,28 @@ __device__ __forceinline__ void bwd_kv_item(
   const int n_pairs = (n_steps + 1) / 2;
 
   // Staging of a step pair: thread chunk i is (step half i >> 1, tensor i & 1 = Q / dO), row
-  // tid >> 4, 16-byte column tid & 15. The dO chunk's row dot product with O gives delta.
+  // tid >> 4, 16-byte column tid & 15, through buffer loads bounded at the document end (rows past
+  // it read as zeros; their lse is +inf, so P = 0). The O chunk of the same row stays in registers
+  // until the store, where its dot product with the dO chunk gives delta = rowsum(dO * O): the
+  // loads are then complete and the dot product does not stall the step.
   const int s_row = tid >> 4, s_col = 8 * (tid & 15);
-  u32x4 sreg[4];
-  float dpart[2];
+  const int s_voff = (s_row * (int)qrow + h * D + s_col) * 2;
+  u32x4 sreg[4], oreg[2];
   float st_lse = 0.f;
+  int st_row = 0;
   auto gload_pair = [&](int p) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int qs0 = k0 + min(2 * p + (i >> 1), n_steps - 1) * BQ;
-      const long row = min(qs0 + s_row, doc_end - 1);
-      const long g = row * qrow + h * D + s_col;
-      sreg[i] = gload16(((i & 1) ? dout : q) + g);
-      if (i & 1) {
-        const u32x4 o8 = gload16(out + g);
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          acc += E::to_f32(half_of(o8, e)) * E::to_f32(half_of(sreg[i], e));
-        dpart[i >> 1] = acc;
-      }
+    for (int sh = 0; sh < 2; ++sh) {
+      const int qs0 = k0 + min(2 * p + sh, n_steps - 1) * BQ;
+      const long base = (long)qs0 * qrow;
+      const long bytes = ((long)(doc_end - qs0 - 1) * qrow + (long)(h + 1) * D) * 2;
+      sreg[2 * sh] = bload16(make_rsrc(q + base, bytes), s_voff);
+      sreg[2 * sh + 1] = bload16(make_rsrc(dout + base, bytes), s_voff);
+      oreg[sh] = bload16(make_rsrc(out + base, bytes), s_voff);
     }
-    if (tid < 64) {
-      const int row = k0 + min(2 * p + (tid >> 5), n_steps - 1) * BQ + (tid & 31);
-      st_lse = row < doc_end ? lse[(long)h * n_tokens + row] * kLog2e : INFINITY;
+    if (tid < 64) {  // raw value: scaled at the store, so that no wait follows the loads here
+      st_row = k0 + min(2 * p + (tid >> 5), n_steps - 1) * BQ + (tid & 31);
+      st_lse = lse[(long)h * n_tokens + min(st_row, doc_end - 1)];
     }
   };
   auto store_pair = [&](int stage) {
@@ -114,14 +112,16 @@ __device__ __forceinline__ void bwd_kv_item(
             sreg[i]);
 #pragma unroll
     for (int sh = 0; sh < 2; ++sh) {  // delta: sum over the 16 threads that share a row
-      float d = dpart[sh];
+      float d = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) d = E::dot2(oreg[sh][w], sreg[2 * sh + 1][w], d);
       d += __shfl_xor(d, 8, 16);
       d += __shfl_xor(d, 4, 16);
       d += __shfl_xor(d, 2, 16);
       d += __shfl_xor(d, 1, 16);
       if ((tid & 15) == 0) stat[stage][sh][1][s_row] = d;
     }
-    if (tid < 64) stat[stage][tid >> 5][0][tid & 31] = st_lse;
+    if (tid < 64) stat[stage][tid >> 5][0][tid & 31] = st_row < doc_end ? st_lse * kLog2e : INFINITY;
   };
 
   const int rm_read = perm32(l32) * LD + 8 * hi;                 // A rows = queries
@@ -192,6 +192,22 @@ __device__ __forceinline__ void bwd_kv_item(
           dkacc[db] = E::mfma(da, ldtr8(qs + off, LD), dkacc[db]);
         }
       }
+      // Software pipeline of the LDS operand reads: 4 MFMAs' operands in flight ahead of the
+      // MFMA that consumes them (S / dP: two b128 reads per MFMA; dV / dK: two transposed reads).
+      VA_SCHED(kSchedDsRead, 8);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        VA_SCHED(kSchedMfma, 1);
+        VA_SCHED(kSchedDsRead, 2);
+      }
+      VA_SCHED(kSchedMfma, 4);
+      VA_SCHED(kSchedDsRead, 8);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        VA_SCHED(kSchedMfma, 1);
+        VA_SCHED(kSchedDsRead, 2);
+      }
+      VA_SCHED(kSchedMfma, 4);
     }
     if (p + 1 < n_pairs) store_pair(stage ^ 1);
     __syncthreads();
@@ -261,7 +277,7 @@ __device__ __forceinline__ void bwd_q_item(
       df[kk] = gload16(dout + g + 16 * kk);
       const u32x4 o8 = gload16(out + g + 16 * kk);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += E::to_f32(half_of(o8, e)) * E::to_f32(half_of(df[kk], e));
+      for (int w = 0; w < 4; ++w) acc = E::dot2(o8[w], df[kk][w], acc);
     }
     dlt = sum_with_other_half(acc);
     lse2 = q_valid ? lse[(long)h * n_tokens + my_q] * kLog2e : INFINITY;
@@ -274,11 +290,14 @@ __device__ __forceinline__ void bwd_q_item(
   // Staging of a tile pair: chunk i is (tile i >> 1, tensor i & 1 = K / V), row tid >> 4.
   const int srow = tid >> 4, scol = 8 * (tid & 15);
   u32x4 sr[4];
-  auto gload_pair = [&](int p) {
+  const int voff = (srow * (int)kvrow + kvh * D + scol) * 2;
+  auto gload_pair = [&](int p) {  // buffer loads bounded at the document end (zero rows: masked)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const long row = min(doc_start + (2 * p + (i >> 1)) * BT + srow, doc_end - 1);
-      sr[i] = gload16(((i & 1) ? v : k) + row * kvrow + kvh * D + scol);
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const int row0 = doc_start + (2 * p + t2) * BT;
+      const long bytes = ((long)(doc_end - row0 - 1) * kvrow + (long)(kvh + 1) * D) * 2;
+      sr[2 * t2] = bload16(make_rsrc(k + (long)row0 * kvrow, bytes), voff);
+      sr[2 * t2 + 1] = bload16(make_rsrc(v + (long)row0 * kvrow, bytes), voff);
     }
   };
   auto store_pair = [&](int stage) {
@@ -299,6 +318,11 @@ __device__ __forceinline__ void bwd_q_item(
 
   gload_pair(0);
   store_pair(0);
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    settle(qf[kk]);
+    settle(df[kk]);
+  }
   __syncthreads();
   for (int p = 0; p < n_pairs; ++p) {
     const int stage = p & 1;

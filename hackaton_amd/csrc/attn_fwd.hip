@@ -30,6 +30,7 @@ constexpr int LD = D + 8;       // LDS row stride (halfs) of the K and V tiles
 constexpr int TILE = BN * LD;   // halfs per K or V tile
 constexpr int PAIR = 4 * TILE;  // K0, V0, K1, V1 of one tile pair
 constexpr int LPT = 4 * BN * 16 / NT;  // 16-byte staging chunks per thread per pair
+constexpr float kRescaleLog2 = 8.f;     // largest P before the running maximum must move
 static_assert(LPT * NT == 4 * BN * 16, "pair staging split");
 static_assert(BM == kFwdBlockM, "the plan's query tile");
 }  // namespace fwd
@@ -69,17 +70,22 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   const int n_pairs = (n_tiles + 1) / 2;
 
   // Staging of one tile pair: chunk i of this thread is tile (i >> 2), tensor ((i >> 1) & 1),
-  // row (tid >> 4) + 32 (i & 1), 16-byte column (tid & 15). Rows clamped to the document.
+  // row (tid >> 4) + 32 (i & 1), 16-byte column (tid & 15). Buffer loads bounded at the document
+  // end: rows past it read as zeros (masked keys, zero P).
   const int srow = tid >> 4, scol = 8 * (tid & 15);
-  const uint16_t* kbase = k + kvh * D + scol;
-  const uint16_t* vbase = v + kvh * D + scol;
+  int voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) voff[i] = (((i >> 1) * BN + srow + 32 * (i & 1)) * (int)kvrow + scol) * 2;
   u32x4 sr[LPT];
   auto gload_pair = [&](int p) {
+    const int row0 = doc_start + 2 * p * BN;
+    const long base = (long)row0 * kvrow + kvh * D;
+    const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
+    const brsrc rk = make_rsrc(k + base, bytes), rv = make_rsrc(v + base, bytes);
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
-      const int t = 2 * p + (i >> 2);
-      const long row = min(doc_start + t * BN + srow + 32 * (i & 1), doc_end - 1);
-      sr[i] = gload16((((i >> 1) & 1) ? vbase : kbase) + row * kvrow);
+      const int c = ((i >> 2) << 1) | (i & 1);
+      sr[i] = bload16(((i >> 1) & 1) ? rv : rk, voff[c]);
     }
   };
   auto store_pair = [&](int stage) {
@@ -104,13 +110,33 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   auto tile = [&](int stage, int t) {
     const int kv0 = doc_start + t * BN;
     const lds_u16* kb = smem + stage * PAIR + kread;
-    f32x16 s[2];
+    // S^T: 16 MFMAs over (kk, b), each K operand read from LDS 4 MFMAs ahead of its use.
+    f32x16 s[2] = {f32x16{}, f32x16{}};
+    u32x4 ka[4];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      s[b] = f32x16{};
+    for (int i = 0; i < 4; ++i) ka[i] = ld128(kb + 32 * (i & 1) * LD + 16 * (i >> 1));
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) s[b] = E::mfma(ld128(kb + 32 * b * LD + 16 * kk), qf[kk], s[b]);
+    for (int i = 0; i < 16; ++i) {
+      const int kk = i >> 1, b = i & 1;
+      s[b] = E::mfma(ka[i & 3], qf[kk], s[b]);
+      if (i + 4 < 16) ka[i & 3] = ld128(kb + 32 * ((i + 4) & 1) * LD + 16 * ((i + 4) >> 1));
     }
+    VA_SCHED(kSchedDsRead, 4);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      VA_SCHED(kSchedMfma, 1);
+      VA_SCHED(kSchedDsRead, 1);
+    }
+    VA_SCHED(kSchedMfma, 4);
+    // The first V^T operands of O^T += V^T P^T, read while the softmax runs.
+    const lds_u16* vb = smem + stage * PAIR + vread;
+    auto v_addr = [&](int i) {  // i = (b, c, db) in MFMA order
+      const int b = i >> 3, c = (i >> 2) & 1, db = i & 3;
+      return vb + (32 * b + 16 * c) * LD + 32 * db;
+    };
+    u32x4 va[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = ldtr8(v_addr(i), LD);
     if (kv0 + BN - 1 > wq0) {  // the tile crosses this strip's diagonal: key > query -> -inf
       const int lim = my_q - kv0;
 #pragma unroll
@@ -125,10 +151,19 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
 #pragma unroll
       for (int j = 0; j < 16; ++j) mt = fmaxf(mt, s[b][j]);
     mt = max_with_other_half(mt) * scale_log2;
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a fully masked first tile
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
+    // The reference maximum m_run moves only when some lane's tile maximum exceeds it by more
+    // than kRescaleLog2 (always on the first tile): P values then stay below 2^kRescaleLog2 and
+    // the O / l rescale is skipped on most tiles. When it moves, every lane takes its exact
+    // running maximum.
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;  // a lane with no visible key yet
     float rs = 0.f;
     u32x4 pf[2][2];
 #pragma unroll
@@ -142,23 +177,19 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
 #pragma unroll
         for (int w = 0; w < 4; ++w) rs = E::sum2(pf[b][c][w], rs);
       }
-    l_run = l_run * alpha + rs;
+    l_run += rs;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
-    const lds_u16* vb = smem + stage * PAIR + vread;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const u32x4 a = ldtr8(vb + (32 * b + 16 * c) * LD + 32 * db, LD);
-          oacc[db] = E::mfma(a, pf[b][c], oacc[db]);
-        }
+    for (int i = 0; i < 16; ++i) {
+      const int b = i >> 3, c = (i >> 2) & 1, db = i & 3;
+      oacc[db] = E::mfma(va[i & 3], pf[b][c], oacc[db]);
+      if (i + 4 < 16) va[i & 3] = ldtr8(v_addr(i + 4), LD);
+    }
   };
 
   gload_pair(0);
   store_pair(0);
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
   __syncthreads();
   for (int p = 0; p < n_pairs; ++p) {
     const int stage = p & 1;

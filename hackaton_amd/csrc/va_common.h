@@ -39,6 +39,11 @@ struct F16 {
   __device__ static inline float sum2(uint32_t x, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), f16x2_t{1, 1}, acc, false);
   }
+  // acc + x.lo * y.lo + x.hi * y.hi in fp32 (v_dot2_f32_f16).
+  __device__ static inline float dot2(uint32_t x, uint32_t y, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, y),
+                                  acc, false);
+  }
 };
 
 struct BF16 {
@@ -57,6 +62,11 @@ struct BF16 {
   __device__ static inline float sum2(uint32_t x, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), bf16x2_t{1, 1}, acc,
                                            false);
+  }
+  // acc + x.lo * y.lo + x.hi * y.hi in fp32 (v_dot2_f32_bf16).
+  __device__ static inline float dot2(uint32_t x, uint32_t y, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x),
+                                           __builtin_bit_cast(bf16x2_t, y), acc, false);
   }
 };
 
@@ -102,6 +112,11 @@ __device__ inline float max_with_other_half(float x) {
   float r0, r1;
   swap_halves(x, r0, r1);
   return fmaxf(r0, r1);
+}
+// The same through ds_bpermute: no inline asm, so it does not end a scheduling region (code that
+// the compiler should interleave with MFMAs uses this one).
+__device__ inline float max_with_other_half_sched(float x) {
+  return fmaxf(x, __shfl_xor(x, 32));
 }
 __device__ inline float sum_with_other_half(float x) {
   float r0, r1;
@@ -183,6 +198,22 @@ __device__ inline u32x4 pack8_tr(const float* v) {
   return pack8<E>(v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]);
 }
 
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+__device__ inline void st64(lds_u16* p, u32x2 v) { *reinterpret_cast<lds_u32x2*>(p) = v; }
+
+// Register transpose of a 4 x 8 block of 16-bit values: r[i] holds row i (8 columns, two per
+// register), c[j] receives column j as {row0 | row1 << 16, row2 | row3 << 16}. v_perm_b32 picks
+// the low (selector 0x05040100) or high (0x07060302) halves of two registers.
+__device__ inline void transpose4x8(const u32x4 (&r)[4], u32x2 (&c)[8]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    c[2 * m] = u32x2{__builtin_amdgcn_perm(r[1][m], r[0][m], 0x05040100u),
+                     __builtin_amdgcn_perm(r[3][m], r[2][m], 0x05040100u)};
+    c[2 * m + 1] = u32x2{__builtin_amdgcn_perm(r[1][m], r[0][m], 0x07060302u),
+                         __builtin_amdgcn_perm(r[3][m], r[2][m], 0x07060302u)};
+  }
+}
+
 __device__ inline u32x4 lds_read16(const uint16_t* base, int elem_off) {
   return *reinterpret_cast<const u32x4*>(base + elem_off);
 }
@@ -191,6 +222,41 @@ __device__ inline void lds_write16(uint16_t* base, int elem_off, u32x4 v) {
 }
 
 __device__ inline u32x4 gload16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Raw buffer resource over [base, base + bytes) (wave-uniform operands, built in SGPRs): a load at
+// a byte offset >= bytes returns zeros, which bounds a tile's rows without per-lane clamping, and
+// the per-lane offset is a 32-bit VGPR that stays fixed while the base moves tile by tile.
+// 0x00020000: the gfx9 buffer descriptor's dword-3 format field for untyped 32-bit data.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+__device__ inline brsrc make_rsrc(const void* base, long bytes) {
+  const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffffL ? 0x7fffffff : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ inline u32x4 bload16(brsrc r, int byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// Buffer load straight into LDS (gfx950 buffer_load_dwordx4 ... lds): lane i's 16 bytes land at
+// dst + 16 i bytes, dst being wave-uniform (it goes through M0). Completion is counted by vmcnt;
+// the compiler does not track the LDS write, so readers wait with wait_vmcnt and a barrier.
+__device__ inline void dma16(brsrc r, lds_u16* dst, int byte_off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           byte_off, 0, 0, 0);
+}
+// s_waitcnt vmcnt(N): at most N vector-memory operations of this wave still outstanding.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// XOR swizzle of the 16 chunks (16 bytes each) of a 256-byte LDS row r: chunk c is stored at
+// c ^ swz16(r). swz16 is a bijection on r mod 16, so the 16 rows that one ds_read_b128 group of
+// lanes reads through perm32 hit 16 different chunks; and for the rows {r0 + 2m} (m = 0..3) of a
+// ds_read_b64_tr_b16 group, bits 2-3 of the swizzle are m, so 4 aligned chunks of each row land
+// on 4 disjoint bank groups.
+__device__ __host__ inline int swz16(int r) {
+  return (((r >> 1) & 3) << 2) | ((r & 1) << 1) | ((r >> 3) & 1);
+}
 __device__ inline void gstore16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 __device__ inline uint16_t half_of(const u32x4& v, int e) {
@@ -205,6 +271,12 @@ constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020,
               kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
 #define VA_SCHED(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Makes the wave wait here until the loads that write `v` have landed. Operands loaded once before
+// a loop and used inside it must be complete at the loop entry: otherwise the counter-based wait
+// inserted before their first use in the loop also waits, on every iteration, for the loads that
+// the loop itself has issued since (the wait counters complete in order).
+__device__ inline void settle(const u32x4& v) { asm volatile("" ::"v"(v)); }
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
