@@ -146,14 +146,36 @@ __device__ __forceinline__ void bwd_kv_item(
     if (s < n_steps && kw0 <= qs0 + BQ - 1) {
       const lds_u16* qs = smem + KV_OFF_Q + (stage * 2 + half) * ROWT;
       const lds_u16* dos = smem + KV_OFF_DO + (stage * 2 + half) * ROWT;
+      // S = Q K^T and dP = dO V^T: 16 MFMAs, both operands of each read from LDS 3 MFMAs ahead.
       f32x16 sacc = f32x16{}, pacc = f32x16{};
+      auto opa = [&](int i) {  // MFMA i: kk = i >> 1, S (i even) or dP (i odd)
+        return ld128(((i & 1) ? dos : qs) + rm_read + 16 * (i >> 1));
+      };
+      auto opb = [&](int i) {
+        return ld128(smem + ((i & 1) ? KV_OFF_V : KV_OFF_K) + kv_read + 16 * (i >> 1));
+      };
+      u32x4 ra[3], rb[3];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        sacc = E::mfma(ld128(qs + rm_read + 16 * kk), ld128(smem + KV_OFF_K + kv_read + 16 * kk),
-                       sacc);
-        pacc = E::mfma(ld128(dos + rm_read + 16 * kk), ld128(smem + KV_OFF_V + kv_read + 16 * kk),
-                       pacc);
+      for (int i = 0; i < 3; ++i) {
+        ra[i] = opa(i);
+        rb[i] = opb(i);
       }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i & 1) pacc = E::mfma(ra[i % 3], rb[i % 3], pacc);
+        else sacc = E::mfma(ra[i % 3], rb[i % 3], sacc);
+        if (i + 3 < 16) {
+          ra[i % 3] = opa(i + 3);
+          rb[i % 3] = opb(i + 3);
+        }
+      }
+      VA_SCHED(kSchedDsRead, 6);
+#pragma unroll
+      for (int i = 0; i < 13; ++i) {
+        VA_SCHED(kSchedMfma, 1);
+        VA_SCHED(kSchedDsRead, 2);
+      }
+      VA_SCHED(kSchedMfma, 3);
       // register j <-> query qs0 + reg_row(j, hi); P overwrites S, dS overwrites dP.
       const lds_f32x4* st = reinterpret_cast<const lds_f32x4*>(
           (__attribute__((address_space(3))) float*)&stat[stage][half][0][0]);
@@ -175,6 +197,9 @@ __device__ __forceinline__ void bwd_kv_item(
             pacc[j] = pv * (pacc[j] - d4[e]);
           }
         }
+      // dV += P^T dO and dK += dS^T Q: 16 MFMAs (c, db, dV / dK), transposed operands read
+      // 3 MFMAs ahead.
+      u32x4 pa[2], da[2];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         float pv8[8], dv8[8];
@@ -183,37 +208,36 @@ __device__ __forceinline__ void bwd_kv_item(
           pv8[e] = sacc[8 * c + e];
           dv8[e] = pacc[8 * c + e];
         }
-        const u32x4 pa = pack8_tr<E>(pv8);
-        const u32x4 da = pack8_tr<E>(dv8);
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const int off = tr_read + 16 * c * LD + 32 * db;
-          dvacc[db] = E::mfma(pa, ldtr8(dos + off, LD), dvacc[db]);
-          dkacc[db] = E::mfma(da, ldtr8(qs + off, LD), dkacc[db]);
-        }
+        pa[c] = pack8_tr<E>(pv8);
+        da[c] = pack8_tr<E>(dv8);
       }
-      // Software pipeline of the LDS operand reads: 4 MFMAs' operands in flight ahead of the
-      // MFMA that consumes them (S / dP: two b128 reads per MFMA; dV / dK: two transposed reads).
-      VA_SCHED(kSchedDsRead, 8);
+      auto opt = [&](int i) {  // MFMA i: c = i >> 3, db = (i >> 1) & 3, dV (i even) / dK (odd)
+        return ldtr8(((i & 1) ? qs : dos) + tr_read + 16 * (i >> 3) * LD + 32 * ((i >> 1) & 3), LD);
+      };
+      u32x4 rt[3];
 #pragma unroll
-      for (int i = 0; i < 12; ++i) {
+      for (int i = 0; i < 3; ++i) rt[i] = opt(i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = i >> 3, db = (i >> 1) & 3;
+        if (i & 1) dkacc[db] = E::mfma(da[c], rt[i % 3], dkacc[db]);
+        else dvacc[db] = E::mfma(pa[c], rt[i % 3], dvacc[db]);
+        if (i + 3 < 16) rt[i % 3] = opt(i + 3);
+      }
+      VA_SCHED(kSchedDsRead, 6);
+#pragma unroll
+      for (int i = 0; i < 13; ++i) {
         VA_SCHED(kSchedMfma, 1);
         VA_SCHED(kSchedDsRead, 2);
       }
-      VA_SCHED(kSchedMfma, 4);
-      VA_SCHED(kSchedDsRead, 8);
-#pragma unroll
-      for (int i = 0; i < 12; ++i) {
-        VA_SCHED(kSchedMfma, 1);
-        VA_SCHED(kSchedDsRead, 2);
-      }
-      VA_SCHED(kSchedMfma, 4);
+      VA_SCHED(kSchedMfma, 3);
     }
     if (p + 1 < n_pairs) store_pair(stage ^ 1);
     __syncthreads();
   }
 
-  // Half 1 hands its partial sums to half 0 (same lane order), which writes this head's dK/dV.
+  // Half 1 hands its partial sums to half 0 (same lane order), which adds them. Register j of
+  // lane (l32, hi) holds key kw0 + 8 (j >> 2) + 4 hi + (j & 3), column d = 32 db + l32.
   float* xk = reinterpret_cast<float*>((uint16_t*)smem);
   if (half == 1) {
 #pragma unroll
@@ -225,21 +249,51 @@ __device__ __forceinline__ void bwd_kv_item(
       }
   }
   __syncthreads();
-  if (half == 1 || kw0 >= doc_end) return;
-  // register j <-> key kw0 + 8 (j >> 2) + 4 hi + (j & 3), column d = 32 db + l32.
+  if (half == 0) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int key = kw0 + 8 * (j >> 2) + 4 * hi + (j & 3);
-    if (key < doc_end) {
-      uint16_t* dkp = dk_part + ((long)key * hq + h) * D + l32;
-      uint16_t* dvp = dv_part + ((long)key * hq + h) * D + l32;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const float dkv = dkacc[db][j] + xk[(strip * 128 + 16 * db + j) * 64 + lane];
-        const float dvv = dvacc[db][j] + xk[(strip * 128 + 64 + 16 * db + j) * 64 + lane];
-        dkp[32 * db] = E::from_f32(dkv * scale);
-        dvp[32 * db] = E::from_f32(dvv);
+      for (int j = 0; j < 16; ++j) {
+        dkacc[db][j] = (dkacc[db][j] + xk[(strip * 128 + 16 * db + j) * 64 + lane]) * scale;
+        dvacc[db][j] += xk[(strip * 128 + 64 + 16 * db + j) * 64 + lane];
       }
+  }
+  __syncthreads();
+  // Half 0 stores the sums as 16-bit values transposed, T[tensor][strip][d][key] (4 consecutive
+  // keys per 8-byte write); then all 8 waves read 8 consecutive d of one key with two transposed
+  // reads and write 16-byte rows of dK / dV (narrow scattered stores would cost 8x the address
+  // work).
+  constexpr int LT = 36;               // row stride (halfs) of T: 32 keys + 4
+  constexpr int TS = D * LT;           // halfs per (tensor, strip) block
+  lds_u16* tt = smem;
+  static_assert(2 * NS * TS <= HALFS, "transposed dK/dV tiles fit in LDS");
+  if (half == 0) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = (32 * db + l32) * LT + 8 * g + 4 * hi;
+        st64(tt + strip * TS + off, u32x2{pack2<E>(dkacc[db][4 * g], dkacc[db][4 * g + 1]),
+                                          pack2<E>(dkacc[db][4 * g + 2], dkacc[db][4 * g + 3])});
+        st64(tt + (NS + strip) * TS + off, u32x2{pack2<E>(dvacc[db][4 * g], dvacc[db][4 * g + 1]),
+                                                 pack2<E>(dvacc[db][4 * g + 2], dvacc[db][4 * g + 3])});
+      }
+  }
+  __syncthreads();
+  // Unit u = (pass, wave, lane group): tensor u >> 7, strip (u >> 5) & 3, 16-key block
+  // (u >> 4) & 1, 8-d chunk u & 15. Source lane s = 4 e + m of the group reads row d0 + e at keys
+  // 16 kb + 4 m; destination lane j receives d0 .. d0 + 3 of key 16 kb + j.
+  const int e4 = src >> 2, m4 = src & 3;
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {
+    const int u = pass * 32 + wave * 4 + grp;
+    const int tensor = u >> 7, st = (u >> 5) & 3, kb = (u >> 4) & 1, dc = u & 15;
+    const lds_u16* base = tt + (tensor * NS + st) * TS + (8 * dc + e4) * LT + 16 * kb + 4 * m4;
+    const u32x2 x = ldtr(base), y = ldtr(base + 4 * LT);
+    const int key = k0 + 32 * st + 16 * kb + src;
+    if (key < doc_end) {
+      uint16_t* dst = (tensor ? dv_part : dk_part) + ((long)key * hq + h) * D + 8 * dc;
+      gstore16(dst, u32x4{x[0], x[1], y[0], y[1]});
     }
   }
 }
