@@ -135,6 +135,7 @@ __device__ __forceinline__ void bwd_kv_item(
     dvacc[db] = f32x16{};
   }
 
+  if (half) __builtin_amdgcn_s_setprio(1);  // see the forward kernel: issue ties between halves
   gload_pair(0);
   store_pair(0);
   __syncthreads();
@@ -370,6 +371,7 @@ __device__ __forceinline__ void bwd_q_item(
 #pragma unroll
   for (int db = 0; db < 4; ++db) dqacc[db] = f32x16{};
 
+  if (half) __builtin_amdgcn_s_setprio(1);  // see the forward kernel: issue ties between halves
   gload_pair(0);
   store_pair(0);
 #pragma unroll

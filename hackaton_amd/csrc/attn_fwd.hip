@@ -186,6 +186,9 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     }
   };
 
+  // The two waves of a SIMD come from different halves; the younger one (half 1) would otherwise
+  // lose every issue tie and finish each pair last, keeping the others at the barrier.
+  if (half) __builtin_amdgcn_s_setprio(1);
   gload_pair(0);
   store_pair(0);
 #pragma unroll
