@@ -339,44 +339,74 @@ def _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scal
     return out, lse, (qr, kr, vr), plan
 
 
+# What PackedAttention keeps for its backward when it does not offload: "outputs" keeps the
+# rotated q/k/v, O and the log-sum-exp in HBM and skips the forward recomputation (one attention
+# forward and one rotation fewer per layer and step, for N * Hq * D * e + 4 * Hq * N bytes more
+# per layer: 6.4 MB per 2048-token layer at the 1.5B shape in fp16); "inputs" keeps q/k/v and recomputes
+# the rotation and the forward in the backward, as solution/attention.py:250-279 does. Both give
+# the same gradients bit for bit (the forward is deterministic). With offload the inputs go to
+# host memory and the forward is recomputed either way (the offloader's contract).
+SAVE_POLICY = "outputs"
+_SAVE_POLICIES = ("outputs", "inputs")
+
+
+def set_save_policy(policy):
+    """Select what PackedAttention keeps for its backward: "outputs" (default) or "inputs"."""
+    global SAVE_POLICY
+    if policy not in _SAVE_POLICIES:
+        raise ValueError(f"save policy must be one of {_SAVE_POLICIES}, got {policy!r}")
+    SAVE_POLICY = policy
+
+
 class PackedAttention(torch.autograd.Function):
     """Rotation + per-sequence causal attention of the packed rows, (N, heads * D) out.
 
-    Keeps only the three projections for the backward (in pinned host memory when `offload`) and
-    recomputes the rotation and the attention forward in the backward, like
-    solution/attention.py:250-279; the backward then runs the attention backward kernels (dK/dV
-    summed over each GQA group in fp32) and the inverse rotation straight from the fp32
-    accumulators. Returns the three projection gradients and 10 Nones."""
+    The backward runs the attention backward kernels (dK/dV summed over each GQA group in fp32)
+    and the inverse rotation straight from the fp32 accumulators. What is kept for it follows
+    SAVE_POLICY: the rotated operands, O and lse ("outputs"), or only the three projections,
+    recomputing the rotation and the forward like solution/attention.py:250-279 ("inputs", and
+    always when `offload` moves them to pinned host memory). Returns the three projection
+    gradients and 10 Nones."""
 
     @staticmethod
     def forward(ctx, q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale,
                 offload):
         with torch.no_grad():
-            out, _lse, _rot, _plan_ = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
-                                              kv_heads, lengths, scale)
+            out, lse, rot, _plan_ = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
+                                            kv_heads, lengths, scale)
         ctx.consts = (cos, sin, b_idx, t_idx)
         ctx.meta = (seq, heads, kv_heads, lengths, scale)
         ctx.dtypes = (q.dtype, k.dtype, v.dtype)
+        ctx.saved_outputs = False
         if offload:
             ctx.item = OFFLOADER.save(q, k, v)
+        elif SAVE_POLICY == "outputs":
+            ctx.saved_outputs = True
+            ctx.save_for_backward(*rot, out, lse)
         else:
             ctx.save_for_backward(q, k, v)
         return out.reshape(q.shape[0], -1).to(_compute_dtype(q.dtype))
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v = OFFLOADER.load(ctx.item) if hasattr(ctx, "item") else ctx.saved_tensors
         cos, sin, b_idx, t_idx = ctx.consts
         seq, heads, kv_heads, lengths, scale = ctx.meta
-        out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
-                                               kv_heads, lengths, scale)
+        if ctx.saved_outputs:
+            qr, kr, vr, out, lse = ctx.saved_tensors
+            plan = _plan(_cu_seqlens([int(x) for x in lengths if int(x) > 0], qr.device), heads,
+                         kv_heads)
+        else:
+            q, k, v = OFFLOADER.load(ctx.item) if hasattr(ctx, "item") else ctx.saved_tensors
+            out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
+                                                   kv_heads, lengths, scale)
         # dq and the per-query-head dK/dV partials; the inverse rotation sums the partials over
         # each GQA group (as solution/attention.py:113-134 sums its expanded copies)
         dq_r, dk_part, dv_part, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
                                                          outputs=False)
+        q_dtype, k_dtype, v_dtype = ctx.dtypes
         dq, dk, dv = rope_backward(dq_r, dk_part, dv_part, cos, sin, b_idx, t_idx, heads,
-                                   kv_heads, q.dtype, expand=True)
-        grads = (dq, dk.to(k.dtype), dv.to(v.dtype))
+                                   kv_heads, q_dtype, expand=True)
+        grads = (dq, dk.to(k_dtype), dv.to(v_dtype))
         return (*grads, None, None, None, None, None, None, None, None, None, None)
 
 

@@ -314,6 +314,45 @@ def test_packed_attention_matches_oracle(dtype):
         assert r <= tol["g"], (name, r)
 
 
+def test_packed_attention_save_policies_agree_bitwise():
+    """Keeping O / lse for the backward ("outputs") gives the same output and gradients, bit for
+    bit, as recomputing the forward in the backward ("inputs", the reference's choice), and keeps
+    the rotated operands plus O and lse instead of the projections."""
+    lengths, heads, kv_heads, dtype = [70, 33, 51, 1, 200], 12, 2, torch.float16
+    banner("packed_attention save policies", lengths)
+    seq = max(lengths)
+    rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)])
+    b_idx, t_idx = (rows // seq).to(torch.int32).cuda(), (rows % seq).to(torch.int32).cuda()
+    n = rows.numel()
+    cos, sin = (t.cuda() for t in rope_tables(seq))
+    g = torch.Generator().manual_seed(3)
+    q = (torch.randn(n, heads * 128, generator=g) * 0.5).to(dtype).cuda()
+    k = (torch.randn(n, kv_heads * 128, generator=g) * 0.5).to(dtype).cuda()
+    v = torch.randn(n, kv_heads * 128, generator=g).to(dtype).cuda()
+    do = torch.randn(n, heads * 128, generator=g).to(dtype).cuda()
+    results = {}
+    try:
+        for policy in ("inputs", "outputs"):
+            att.set_save_policy(policy)
+            qd, kd, vd = (t.clone().requires_grad_() for t in (q, k, v))
+            out = att.packed_attention(qd, kd, vd, cos, sin, b_idx, t_idx, seq, heads, kv_heads,
+                                       lengths, SCALE)
+            saved = [t.shape for t in out.grad_fn.saved_tensors]
+            out.backward(do)
+            torch.cuda.synchronize()
+            results[policy] = (out.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu(),
+                               saved)
+    finally:
+        att.set_save_policy("outputs")
+    for a, b in zip(results["inputs"][:4], results["outputs"][:4]):
+        assert torch.equal(a, b)
+    assert results["inputs"][4] == [q.shape, k.shape, v.shape]
+    assert results["outputs"][4] == [(n, heads, 128), (n, kv_heads, 128), (n, kv_heads, 128),
+                                     (n, heads, 128), (heads, n)]
+    with pytest.raises(ValueError):
+        att.set_save_policy("everything")
+
+
 def test_packed_attention_offloaded_matches_plain_autograd(monkeypatch):
     """solution/test_offload.py:68-106: three offloaded layers, forward bitwise equal, grads
     within 1e-2 of 3x the single call."""
