@@ -29,6 +29,8 @@ SIGNATURES = {
     "va_head_dim": (_i32, []),
     "va_plan_size": (ctypes.c_int, [_pi32, _i32, _i32, _i32, _i32, _pi64]),
     "va_plan_build": (ctypes.c_int, [_pi32, _i32, _i32, _i32, _i32, _pi32, _i64, _pi64]),
+    "va_plan_capacity": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64]),
+    "va_plan_build_device": (ctypes.c_int, [_p, _i32, _i64, _i32, _i32, _i32, _p, _i64, _p]),
     "va_fwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _i32,
                               _p]),
     "va_bwd_workspace_layout": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64, _pi64]),

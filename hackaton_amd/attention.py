@@ -118,8 +118,43 @@ def build_plan_host(cu, hq, hkv, kind):
     return items[: int(n[0])]
 
 
-def _plan(cu_seqlens, hq, hkv):
+class DevicePlan:
+    """Work lists built on the device from a device cu_seqlens (va_plan_build_device): no host
+    read of the lengths. Each list has the capacity that the host-known sizes bound; its slots past
+    the real items are empty items that the kernels skip."""
+
+    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total")
+
+    def __init__(self, cu_seqlens, n_tokens, hq, hkv):
+        n_docs = cu_seqlens.shape[0] - 1
+        self.total = int(n_tokens)
+        stream = _stream()
+        lists = []
+        for kind in (_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD):
+            cap = np.zeros(1, dtype=np.int64)
+            check(lib().va_plan_capacity(n_tokens, n_docs, hq, kind, cap.ctypes.data_as(_lib._pi64)),
+                  "va_plan_capacity")
+            items = torch.empty(max(int(cap[0]), 1), 4, dtype=torch.int32,
+                                device=cu_seqlens.device)
+            check(lib().va_plan_build_device(cu_seqlens.data_ptr(), n_docs, n_tokens, hq, hkv, kind,
+                                             items.data_ptr(), int(cap[0]), stream),
+                  "va_plan_build_device")
+            lists.append((items, int(cap[0])))
+        (self.fwd_items, self.n_fwd), (self.bwd_items, self.n_bwd) = lists
+
+
+def _device_cu_seqlens(lengths):
+    """int32 [0, l0, l0 + l1, ...] on the device from a device tensor of lengths, with no host
+    read (zero lengths are empty documents: they produce no work)."""
+    cu = torch.zeros(lengths.numel() + 1, dtype=torch.int32, device=lengths.device)
+    cu[1:] = torch.cumsum(lengths.reshape(-1).to(torch.int64).clamp(min=0), 0).to(torch.int32)
+    return cu
+
+
+def _plan(cu_seqlens, hq, hkv, n_tokens=None):
     offsets = getattr(cu_seqlens, "_va_offsets", None)
+    if offsets is None and n_tokens is not None and cu_seqlens.is_cuda:
+        return DevicePlan(cu_seqlens, n_tokens, hq, hkv)
     if offsets is None:  # a cu_seqlens tensor not made by _cu_seqlens: read it (one sync)
         offsets = tuple(int(x) for x in cu_seqlens.cpu().tolist())
     key = (cu_seqlens.device, offsets, hq, hkv)
@@ -207,7 +242,7 @@ class VarlenAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query, key, value, cu_seqlens, max_len, scale):
-        plan = _plan(cu_seqlens, query.shape[1], key.shape[1])
+        plan = _plan(cu_seqlens, query.shape[1], key.shape[1], query.shape[0])
         out, lse = attention_forward(query, key, value, plan, scale)
         ctx.save_for_backward(query, key, value, out, lse, cu_seqlens)
         ctx.max_len, ctx.scale, ctx.plan = max_len, scale, plan
@@ -220,13 +255,23 @@ class VarlenAttention(torch.autograd.Function):
         return dq, dk, dv, None, None, None
 
 
+def _lengths_cu(lengths, device):
+    """cu_seqlens for `lengths`: a host list (zero lengths dropped, as solution/attention.py:239;
+    the plan is built on the host and cached) or a device tensor (cu_seqlens and the plan are
+    built on the device: no host read, no synchronisation)."""
+    if isinstance(lengths, torch.Tensor) and lengths.is_cuda:
+        return _device_cu_seqlens(lengths), None
+    lengths = [int(length) for length in lengths if int(length) > 0]
+    return _cu_seqlens(lengths, device), max(lengths)
+
+
 def varlen_attention(query, key, value, lengths, scale):
     """Causal attention of each sequence on its own, on packed (N, H, D) rows where sequence i is
-    the contiguous block of `lengths[i]` rows; returns (N, H * D). solution/attention.py:236-242."""
-    lengths = [int(length) for length in lengths if int(length) > 0]
-    cu_seqlens = _cu_seqlens(lengths, query.device)
+    the contiguous block of `lengths[i]` rows; returns (N, H * D). solution/attention.py:236-242.
+    `lengths` may also be a device tensor: then nothing is read back to the host."""
+    cu_seqlens, max_len = _lengths_cu(lengths, query.device)
     return VarlenAttention.apply(query.contiguous(), key.contiguous(), value.contiguous(),
-                                 cu_seqlens, max(lengths), scale)
+                                 cu_seqlens, max_len, scale)
 
 
 # ------------------------------------------------------------------------------------------------
@@ -330,9 +375,8 @@ def _compute_dtype(proj_dtype):
 def _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale):
     """Rotation (no K/V expansion) + varlen attention; returns (out (N,Hq,D), lse, rotated q/k/v,
     plan). solution/attention.py:245-247."""
-    lengths = [int(length) for length in lengths if int(length) > 0]
-    cu = _cu_seqlens(lengths, q.device)
-    plan = _plan(cu, heads, kv_heads)
+    cu, _max_len = _lengths_cu(lengths, q.device)
+    plan = _plan(cu, heads, kv_heads, q.shape[0])
     qr, kr, vr = rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads,
                               _compute_dtype(q.dtype))
     out, lse = attention_forward(qr, kr, vr, plan, scale)
@@ -372,8 +416,8 @@ class PackedAttention(torch.autograd.Function):
     def forward(ctx, q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale,
                 offload):
         with torch.no_grad():
-            out, lse, rot, _plan_ = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
-                                            kv_heads, lengths, scale)
+            out, lse, rot, plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads,
+                                          lengths, scale)
         ctx.consts = (cos, sin, b_idx, t_idx)
         ctx.meta = (seq, heads, kv_heads, lengths, scale)
         ctx.dtypes = (q.dtype, k.dtype, v.dtype)
@@ -382,6 +426,7 @@ class PackedAttention(torch.autograd.Function):
             ctx.item = OFFLOADER.save(q, k, v)
         elif SAVE_POLICY == "outputs":
             ctx.saved_outputs = True
+            ctx.plan = plan
             ctx.save_for_backward(*rot, out, lse)
         else:
             ctx.save_for_backward(q, k, v)
@@ -393,8 +438,7 @@ class PackedAttention(torch.autograd.Function):
         seq, heads, kv_heads, lengths, scale = ctx.meta
         if ctx.saved_outputs:
             qr, kr, vr, out, lse = ctx.saved_tensors
-            plan = _plan(_cu_seqlens([int(x) for x in lengths if int(x) > 0], qr.device), heads,
-                         kv_heads)
+            plan = ctx.plan
         else:
             q, k, v = OFFLOADER.load(ctx.item) if hasattr(ctx, "item") else ctx.saved_tensors
             out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,

@@ -454,6 +454,7 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][half][lse|del]
   lds_u16* smem = (lds_u16*)smem_raw;
   const int4 it = items[blockIdx.x];
+  if (it.x >= it.y) return;  // an empty slot of a device-built plan
   if ((it.w >> 24) == bwd::kKindKV) {
     bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,
                    scale, scale_log2);

@@ -46,6 +46,7 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
 
   const int4 it = items[blockIdx.x];
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w;
+  if (q0 >= doc_end) return;  // an empty slot of a device-built plan
   const int group = hq / hkv;
   const int kvh = h / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;

@@ -5,7 +5,10 @@
 // tiles and cross-document tiles are never launched. Items are ordered by decreasing work
 // (longest-processing-time first): the hardware dispatcher hands work-groups out in index order,
 // so the longest tiles start first and the short ones fill the tail.
+#include <hip/hip_runtime.h>
+
 #include <algorithm>
+#include <climits>
 #include <cstdint>
 #include <vector>
 
@@ -114,5 +117,39 @@ extern "C" int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t 
     items[4 * i + 2] = v[i].c;
     items[4 * i + 3] = v[i].d;
   }
+  return VA_OK;
+}
+
+extern "C" int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t kind,
+                                int64_t* capacity) {
+  if (capacity == nullptr) return va::fail(VA_EINVAL, "capacity is NULL");
+  if (kind != VA_PLAN_FWD && kind != VA_PLAN_BWD) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
+  if (n_tokens < 0 || n_tokens > INT32_MAX / 2)
+    return va::fail(VA_ESHAPE, "n_tokens=%lld out of range", (long long)n_tokens);
+  if (n_docs < 0 || n_docs > va::kPlanMaxDocs)
+    return va::fail(VA_ESHAPE, "n_docs=%d out of range [0, %d]", n_docs, va::kPlanMaxDocs);
+  if (hq <= 0 || hq > 4096) return va::fail(VA_ESHAPE, "Hq=%d out of range", hq);
+  const int64_t tiles = (n_tokens + va::kFwdBlockM - 1) / va::kFwdBlockM + n_docs;
+  *capacity = tiles * hq * (kind == VA_PLAN_FWD ? 1 : 2);
+  return VA_OK;
+}
+
+extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs,
+                                    int64_t n_tokens, int32_t hq, int32_t hkv, int32_t kind,
+                                    int32_t* items_device, int64_t capacity, void* stream) {
+  int64_t need = 0;
+  int rc = va_plan_capacity(n_tokens, n_docs, hq, kind, &need);
+  if (rc) return rc;
+  rc = check_heads(hq, hkv);
+  if (rc) return rc;
+  if (cu_seqlens_device == nullptr || items_device == nullptr)
+    return va::fail(VA_EINVAL, "cu_seqlens_device / items_device is NULL");
+  if (((uintptr_t)items_device & 15u) != 0) return va::fail(VA_EINVAL, "items_device not 16-byte aligned");
+  if (capacity < need)
+    return va::fail(VA_ECAPACITY, "device plan needs capacity %lld, got %lld", (long long)need,
+                    (long long)capacity);
+  const hipError_t e = va::launch_plan_device(cu_seqlens_device, n_docs, (int)n_tokens, hq, kind,
+                                              items_device, (long)capacity, (hipStream_t)stream);
+  if (e != hipSuccess) return va::fail((int)e, "va_plan_build_device launch: %s", hipGetErrorString(e));
   return VA_OK;
 }

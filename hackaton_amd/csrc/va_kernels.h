@@ -15,6 +15,7 @@ constexpr int kBwdBlockN = 128;  // keys per backward kv work item
 constexpr int kBwdBlockQ = 32;   // queries per kv-item step
 constexpr int kBwdBlockM = 128;  // queries per backward q work item
 constexpr int kBwdTileK = 32;    // keys per q-item tile
+constexpr int kPlanMaxDocs = 8192;  // documents a device-built plan takes (LDS-resident bounds)
 
 struct FwdArgs {
   const void* q;
@@ -84,5 +85,9 @@ hipError_t launch_rope_bwd(const RopeArgs& a);
 hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t* t_idx,
                             int64_t n_tokens, int heads, int seq, int row_bytes, int mode,
                             hipStream_t stream);
+
+// Device-built plan (plan_device.hip): `capacity` items, real ones first, empty ones after.
+hipError_t launch_plan_device(const int32_t* cu, int n_docs, int n_tokens, int hq, int kind,
+                              int32_t* items, long capacity, hipStream_t stream);
 
 }  // namespace va

@@ -65,6 +65,21 @@ int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t 
 int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                   int32_t* items, int64_t capacity, int64_t* n_items);
 
+/* ---- work plan built on the device --------------------------------------------------------------
+ * For callers whose document lengths live on the GPU: the plan is built from a device cu_seqlens
+ * by one kernel on `stream`, with no host read (the reference reads the lengths back with
+ * lengths.tolist(), solution/packed.py:170-172, before _cu_seqlens at attention.py:195-209).
+ * va_plan_capacity gives, from host-known sizes only, the number of items such a plan has:
+ * ceil(n_tokens / 128) + n_docs tiles per query head, twice that for VA_PLAN_BWD.
+ * va_plan_build_device writes exactly `capacity` items (int32 x 4) to device memory: the real
+ * ones longest first, then empty items that va_fwd / va_bwd skip, so the kernels take n_items =
+ * capacity. Document bounds are clamped into [0, n_tokens] and made non-decreasing on the device.
+ * n_docs <= 8192. */
+int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t kind, int64_t* capacity);
+int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs, int64_t n_tokens,
+                         int32_t hq, int32_t hkv, int32_t kind, int32_t* items_device,
+                         int64_t capacity, void* stream);
+
 /* ---- attention forward ------------------------------------------------------------------------
  * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row;
  * scale must be finite and > 0 (D^-0.5 in the reference).

@@ -143,3 +143,35 @@ def test_product_path_refuses_cpu_tensors():
     k = torch.zeros(8, 2, 128, dtype=torch.float16)
     with pytest.raises(ValueError, match="GPU only"):
         varlen_attention(q, k, k, [8], 0.1)
+
+
+@pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1, 1, 1], [129, 0, 300],
+                                     [4096, 17], [127, 128, 129]])
+@pytest.mark.parametrize("kind", [_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD])
+def test_device_plan_capacity_bounds_the_host_plan(lengths, kind):
+    """va_plan_capacity, from host-known sizes only, is never below the real item count."""
+    hq = 12
+    cu, items = plan(lengths, hq, 2, kind)
+    cap = np.zeros(1, dtype=np.int64)
+    assert _lib.lib().va_plan_capacity(int(cu[-1]), len(lengths), hq, kind,
+                                       cap.ctypes.data_as(_lib._pi64)) == 0
+    assert int(cap[0]) >= len(items)
+    tiles = -(-int(cu[-1]) // 128) + len(lengths)
+    assert int(cap[0]) == tiles * hq * (1 if kind == _lib.VA_PLAN_FWD else 2)
+
+
+def test_device_plan_rejects_bad_arguments_before_launching():
+    lib = _lib.lib()
+    cap = np.zeros(1, dtype=np.int64)
+    p = cap.ctypes.data_as(_lib._pi64)
+    assert lib.va_plan_capacity(100, 9000, 12, _lib.VA_PLAN_FWD, p) == _lib.VA_ESHAPE  # > 8192
+    assert lib.va_plan_capacity(-1, 1, 12, _lib.VA_PLAN_FWD, p) == _lib.VA_ESHAPE
+    assert lib.va_plan_capacity(100, 1, 12, 7, p) == _lib.VA_EINVAL
+    # capacity below the bound, NULL pointers and bad heads fail before any device call
+    assert lib.va_plan_build_device(None, 1, 100, 12, 2, _lib.VA_PLAN_FWD, None, 100,
+                                    None) == _lib.VA_EINVAL
+    fake = ctypes.c_void_p(4096)
+    assert lib.va_plan_build_device(fake, 1, 100, 12, 2, _lib.VA_PLAN_FWD, fake, 1,
+                                    None) == _lib.VA_ECAPACITY
+    assert lib.va_plan_build_device(fake, 1, 100, 12, 5, _lib.VA_PLAN_FWD, fake, 1000,
+                                    None) == _lib.VA_ESHAPE

@@ -314,6 +314,48 @@ def test_packed_attention_matches_oracle(dtype):
         assert r <= tol["g"], (name, r)
 
 
+@pytest.mark.parametrize("lengths", [[64, 37, 50, 12], [334, 0, 200, 100, 7], [1000, 24],
+                                     [1, 1, 1, 2, 3]])
+def test_device_plan_matches_host_plan(lengths):
+    """The plan built on the device from a device cu_seqlens holds the host plan's items (as a
+    set: the order inside a work bucket is free), then empty items up to its capacity; zero
+    lengths make no items."""
+    banner("device plan", lengths)
+    hq, hkv = 12, 2
+    dev = torch.device("cuda")
+    cu_dev = att._device_cu_seqlens(torch.tensor(lengths, device=dev))
+    n = sum(lengths)
+    dplan = att.DevicePlan(cu_dev, n, hq, hkv)
+    torch.cuda.synchronize()
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    for kind, items, count in ((0, dplan.fwd_items, dplan.n_fwd), (1, dplan.bwd_items, dplan.n_bwd)):
+        host = att.build_plan_host(cu, hq, hkv, kind)
+        got = items.cpu().numpy()[:count]
+        real, empty = got[: len(host)], got[len(host):]
+        assert sorted(map(tuple, real.tolist())) == sorted(map(tuple, host.tolist()))
+        assert not empty.any()
+        # longest first by the planner's work measure (buckets of 8 apart)
+        if kind == 0:
+            work = [min(q0 + 128, e) - s for q0, e, s, _ in real.tolist()]
+            assert all(a // 8 >= b // 8 for a, b in zip(work, work[1:]))
+
+
+def test_device_lengths_run_without_host_reads_and_match_host_lengths():
+    """varlen_attention and packed_attention with the lengths as a device tensor (device
+    cu_seqlens and plan, no host read) give bitwise the host-lengths results."""
+    lengths, hq, hkv = [334, 200, 0, 100, 7], 12, 2
+    banner("device lengths", lengths)
+    q, k, v, do = wl.make_inputs([x for x in lengths if x], hq, hkv, torch.float16, seed=5)
+    host = run_varlen(q, k, v, do, lengths)
+    dev_lengths = torch.tensor(lengths, device="cuda")
+    qd, kd, vd = (t.cuda().requires_grad_() for t in (q, k, v))
+    out = att.varlen_attention(qd, kd, vd, dev_lengths, SCALE)
+    out.backward(do.cuda().reshape(out.shape))
+    torch.cuda.synchronize()
+    for a, b in zip(host, (out.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu())):
+        assert torch.equal(a, b)
+
+
 def test_packed_attention_save_policies_agree_bitwise():
     """Keeping O / lse for the backward ("outputs") gives the same output and gradients, bit for
     bit, as recomputing the forward in the backward ("inputs", the reference's choice), and keeps
