@@ -14,6 +14,8 @@
 //            lane, lse and delta in-lane), dS^T, dQ^T += K^T dS^T. The halves add their dQ through
 //            LDS and write it once in the element type.
 //  finish    dK/dV = sum over the G query heads of each group of the per-head partials.
+#include <type_traits>
+
 #include "va_common.h"
 #include "va_kernels.h"
 
@@ -180,24 +182,35 @@ __device__ __forceinline__ void bwd_kv_item(
       // register j <-> query qs0 + reg_row(j, hi); P overwrites S, dS overwrites dP.
       const lds_f32x4* st = reinterpret_cast<const lds_f32x4*>(
           (__attribute__((address_space(3))) float*)&stat[stage][half][0][0]);
-      const bool diag = kw0 + 31 > qs0;
-      const int lim = my_key - qs0;
+      // The dV / dK operands do not depend on the softmax: their first reads go out before it.
+      auto opt = [&](int i) {  // MFMA i: c = i >> 3, db = (i >> 1) & 3, dV (i even) / dK (odd)
+        return ldtr8(((i & 1) ? qs : dos) + tr_read + 16 * (i >> 3) * LD + 32 * ((i >> 1) & 3), LD);
+      };
+      u32x4 rt[3];
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int i = 0; i < 3; ++i) rt[i] = opt(i);
+      __builtin_amdgcn_sched_barrier(0);
+      auto softmax = [&](auto masked) {
+        const int lim = my_key - qs0;
 #pragma unroll
-        for (int g4 = 0; g4 < 2; ++g4) {
-          const int r0 = 16 * c + 8 * hi + 4 * g4;
-          const f32x4 l4 = st[r0 / 4];
-          const f32x4 d4 = st[(BQ + r0) / 4];
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = 8 * c + 4 * g4 + e;
-            float pv = fast_exp2(fmaf(sacc[j], scale_log2, -l4[e]));
-            if (diag && reg_row(j, hi) < lim) pv = 0.f;  // key > query
-            sacc[j] = pv;
-            pacc[j] = pv * (pacc[j] - d4[e]);
+          for (int g4 = 0; g4 < 2; ++g4) {
+            const int r0 = 16 * c + 8 * hi + 4 * g4;
+            const f32x4 l4 = st[r0 / 4];
+            const f32x4 d4 = st[(BQ + r0) / 4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = 8 * c + 4 * g4 + e;
+              float pv = fast_exp2(fmaf(sacc[j], scale_log2, -l4[e]));
+              if (masked && reg_row(j, hi) < lim) pv = 0.f;  // key > query
+              sacc[j] = pv;
+              pacc[j] = pv * (pacc[j] - d4[e]);
+            }
           }
-        }
+      };
+      if (kw0 + 31 > qs0) softmax(std::true_type{});  // the step crosses this strip's diagonal
+      else softmax(std::false_type{});
       // dV += P^T dO and dK += dS^T Q: 16 MFMAs (c, db, dV / dK), transposed operands read
       // 3 MFMAs ahead.
       u32x4 pa[2], da[2];
@@ -212,26 +225,14 @@ __device__ __forceinline__ void bwd_kv_item(
         pa[c] = pack8_tr<E>(pv8);
         da[c] = pack8_tr<E>(dv8);
       }
-      auto opt = [&](int i) {  // MFMA i: c = i >> 3, db = (i >> 1) & 3, dV (i even) / dK (odd)
-        return ldtr8(((i & 1) ? qs : dos) + tr_read + 16 * (i >> 3) * LD + 32 * ((i >> 1) & 3), LD);
-      };
-      u32x4 rt[3];
-#pragma unroll
-      for (int i = 0; i < 3; ++i) rt[i] = opt(i);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int c = i >> 3, db = (i >> 1) & 3;
         if (i & 1) dkacc[db] = E::mfma(da[c], rt[i % 3], dkacc[db]);
         else dvacc[db] = E::mfma(pa[c], rt[i % 3], dvacc[db]);
         if (i + 3 < 16) rt[i % 3] = opt(i + 3);
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads 3 MFMAs ahead: not sunk to their use
       }
-      VA_SCHED(kSchedDsRead, 6);
-#pragma unroll
-      for (int i = 0; i < 13; ++i) {
-        VA_SCHED(kSchedMfma, 1);
-        VA_SCHED(kSchedDsRead, 2);
-      }
-      VA_SCHED(kSchedMfma, 3);
     }
     if (p + 1 < n_pairs) store_pair(stage ^ 1);
     __syncthreads();
@@ -387,28 +388,48 @@ __device__ __forceinline__ void bwd_q_item(
     const int kv0 = doc_start + t * BT;
     if (t < n_tiles && kv0 <= wq0 + 31) {
       const lds_u16* base = smem + stage * Q_PAIR;
+      // S^T = K Q^T and dP^T = V dO^T: 16 MFMAs, the K / V operand read 3 MFMAs ahead.
       f32x16 sacc = f32x16{}, pacc = f32x16{};
+      auto opa = [&](int i) {  // MFMA i: kk = i >> 1, S (i even) or dP (i odd)
+        return ld128(base + ((i & 1) ? va_read : ka_read) + 16 * (i >> 1));
+      };
+      u32x4 ra[3];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        sacc = E::mfma(ld128(base + ka_read + 16 * kk), qf[kk], sacc);
-        pacc = E::mfma(ld128(base + va_read + 16 * kk), df[kk], pacc);
+      for (int i = 0; i < 3; ++i) ra[i] = opa(i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i & 1) pacc = E::mfma(ra[i % 3], df[i >> 1], pacc);
+        else sacc = E::mfma(ra[i % 3], qf[i >> 1], sacc);
+        if (i + 3 < 16) ra[i % 3] = opa(i + 3);
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead: not sunk to their use
       }
+      // dQ^T operands (K^T, transposed reads) do not depend on the softmax: the first go out now.
+      auto opt = [&](int i) {  // MFMA i: c = i >> 2, db = i & 3
+        return ldtr8(base + kt_read + 16 * (i >> 2) * LD + 32 * (i & 3), LD);
+      };
+      u32x4 rt[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) rt[i] = opt(i);
+      __builtin_amdgcn_sched_barrier(0);
       // register j <-> key kv0 + reg_row(j, hi), query my_q.
-      const bool diag = kv0 + 31 > wq0;
-      const int lim = my_q - kv0;
       float ds[16];
+      auto softmax = [&](auto masked) {
+        const int lim = my_q - kv0;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float pv = fast_exp2(fmaf(sacc[j], scale_log2, -lse2));
-        if (diag && reg_row(j, hi) > lim) pv = 0.f;  // key > query
-        ds[j] = pv * (pacc[j] - dlt);
-      }
+        for (int j = 0; j < 16; ++j) {
+          float pv = fast_exp2(fmaf(sacc[j], scale_log2, -lse2));
+          if (masked && reg_row(j, hi) > lim) pv = 0.f;  // key > query
+          ds[j] = pv * (pacc[j] - dlt);
+        }
+      };
+      if (kv0 + 31 > wq0) softmax(std::true_type{});  // the tile crosses this strip's diagonal
+      else softmax(std::false_type{});
+      const u32x4 bf[2] = {pack8_tr<E>(ds), pack8_tr<E>(ds + 8)};
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const u32x4 bf = pack8_tr<E>(ds + 8 * c);
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-          dqacc[db] = E::mfma(ldtr8(base + kt_read + 16 * c * LD + 32 * db, LD), bf, dqacc[db]);
+      for (int i = 0; i < 8; ++i) {
+        dqacc[i & 3] = E::mfma(rt[i % 3], bf[i >> 2], dqacc[i & 3]);
+        if (i + 3 < 8) rt[i % 3] = opt(i + 3);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (p + 1 < n_pairs) store_pair(stage ^ 1);
