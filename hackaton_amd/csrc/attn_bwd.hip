@@ -4,9 +4,11 @@
 //  kv item   128 keys of one document x one query head, 8 waves: 4 key strips of 32 x 2 halves
 //            that take alternate 32-query steps (two waves per SIMD). Per step: S = Q K^T and
 //            dP = dO V^T (rows = queries), P = exp2(S scale log2e - lse log2e), dS = P (dP - delta),
-//            dV += P^T dO and dK += dS^T Q with the transposed operands read by ds_read_b64_tr_b16.
-//            delta = rowsum(dO * O) is computed by the staging threads. The halves add their partial
-//            dK/dV through LDS and write them once, per query head: into dK/dV themselves when
+//            dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read by ds_read_b64_tr_b16, so that
+//            a lane holds 8 consecutive d of one key per 8 accumulator registers. delta =
+//            rowsum(dO * O) is computed by the staging threads. The halves add their partial
+//            dK/dV through LDS (half 0 finishes dK, half 1 dV) and write them once, 16-byte rows
+//            straight from registers, per query head: into dK/dV themselves when
 //            Hq == Hkv, else into per-head partials that the finish pass (or the rotary backward)
 //            sums over each GQA group, as the reference sums its expanded copies.
 //  q item    128 queries of one document x one query head, 8 waves: 4 query strips x 2 halves that
@@ -43,7 +45,6 @@ constexpr int Q_PAIR = 4 * ROWT;
 constexpr int Q_HALFS = 2 * Q_PAIR;
 constexpr int HALFS = KV_HALFS > Q_HALFS ? KV_HALFS : Q_HALFS;
 static_assert(BK == kBwdBlockN && QB == kBwdBlockM && BQ == kBwdBlockQ, "plan tile sizes");
-static_assert(NS * 128 * 64 * 4 <= HALFS * 2, "dK/dV exchange fits in LDS");
 constexpr int kKindKV = 0, kKindQ = 1;
 }  // namespace bwd
 
@@ -128,7 +129,10 @@ __device__ __forceinline__ void bwd_kv_item(
 
   const int rm_read = perm32(l32) * LD + 8 * hi;                 // A rows = queries
   const int kv_read = (32 * strip + l32) * LD + 8 * hi;          // B columns = keys
-  const int tr_read = (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) + 4 * (src & 3);
+  // Q^T / dO^T rows (d) through transposed reads, columns in the order that makes the 8
+  // registers [8c, 8c + 8) of a dK^T / dV^T accumulator 8 consecutive d (16-byte stores).
+  const int tr_read = (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) +
+                      4 * ((((src & 3) & 1) << 1) | ((src & 3) >> 1));
 
   f32x16 dkacc[4], dvacc[4];
 #pragma unroll
@@ -211,8 +215,8 @@ __device__ __forceinline__ void bwd_kv_item(
       };
       if (kw0 + 31 > qs0) softmax(std::true_type{});  // the step crosses this strip's diagonal
       else softmax(std::false_type{});
-      // dV += P^T dO and dK += dS^T Q: 16 MFMAs (c, db, dV / dK), transposed operands read
-      // 3 MFMAs ahead.
+      // dV^T += dO^T P and dK^T += Q^T dS: 16 MFMAs (c, db, dV / dK), the transposed operands
+      // read 3 MFMAs ahead.
       u32x4 pa[2], da[2];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -228,8 +232,8 @@ __device__ __forceinline__ void bwd_kv_item(
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int c = i >> 3, db = (i >> 1) & 3;
-        if (i & 1) dkacc[db] = E::mfma(da[c], rt[i % 3], dkacc[db]);
-        else dvacc[db] = E::mfma(pa[c], rt[i % 3], dvacc[db]);
+        if (i & 1) dkacc[db] = E::mfma(rt[i % 3], da[c], dkacc[db]);
+        else dvacc[db] = E::mfma(rt[i % 3], pa[c], dvacc[db]);
         if (i + 3 < 16) rt[i % 3] = opt(i + 3);
         __builtin_amdgcn_sched_barrier(0);  // keep the reads 3 MFMAs ahead: not sunk to their use
       }
@@ -238,66 +242,42 @@ __device__ __forceinline__ void bwd_kv_item(
     __syncthreads();
   }
 
-  // Half 1 hands its partial sums to half 0 (same lane order), which adds them. Register j of
-  // lane (l32, hi) holds key kw0 + 8 (j >> 2) + 4 hi + (j & 3), column d = 32 db + l32.
-  float* xk = reinterpret_cast<float*>((uint16_t*)smem);
-  if (half == 1) {
+  // dK^T / dV^T: register j of lane (l32, hi) of accumulator db holds key kw0 + l32 and
+  // d = 32 db + reg_row(j, hi), so registers [8c, 8c + 8) are d 32 db + 16 c + 8 hi + 0..7.
+  // The halves swap one tensor each through LDS (16-byte chunks, same lane order): half 0 adds
+  // half 1's dK and writes dK (scaled), half 1 adds half 0's dV and writes dV.
+  lds_f32x4* xs = reinterpret_cast<lds_f32x4*>(
+      (__attribute__((address_space(3))) float*)(smem));
+  auto slot = [&](int tensor, int db, int j4) { return ((tensor * NS + strip) * 16 + 4 * db + j4) * 64 + lane; };
+  static_assert(2 * NS * 16 * 64 * 16 <= HALFS * 2, "dK/dV exchange fits in LDS");
+  auto finish = [&](f32x16(&mine)[4], const f32x16(&other)[4], float mul, uint16_t* part) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        xk[(strip * 128 + 16 * db + j) * 64 + lane] = dkacc[db][j];
-        xk[(strip * 128 + 64 + 16 * db + j) * 64 + lane] = dvacc[db][j];
+      for (int j4 = 0; j4 < 4; ++j4)
+        xs[slot(half ^ 1, db, j4)] = f32x4{other[db][4 * j4], other[db][4 * j4 + 1],
+                                           other[db][4 * j4 + 2], other[db][4 * j4 + 3]};
+    __syncthreads();
+    if (my_key >= doc_end) return;
+    uint16_t* dst = part + ((long)my_key * hq + h) * D + 8 * hi;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      float x[16];
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const f32x4 y = xs[slot(half, db, j4)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[4 * j4 + e] = (mine[db][4 * j4 + e] + y[e]) * mul;
       }
-  }
-  __syncthreads();
-  if (half == 0) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        dkacc[db][j] = (dkacc[db][j] + xk[(strip * 128 + 16 * db + j) * 64 + lane]) * scale;
-        dvacc[db][j] += xk[(strip * 128 + 64 + 16 * db + j) * 64 + lane];
-      }
-  }
-  __syncthreads();
-  // Half 0 stores the sums as 16-bit values transposed, T[tensor][strip][d][key] (4 consecutive
-  // keys per 8-byte write); then all 8 waves read 8 consecutive d of one key with two transposed
-  // reads and write 16-byte rows of dK / dV (narrow scattered stores would cost 8x the address
-  // work).
-  constexpr int LT = 36;               // row stride (halfs) of T: 32 keys + 4
-  constexpr int TS = D * LT;           // halfs per (tensor, strip) block
-  lds_u16* tt = smem;
-  static_assert(2 * NS * TS <= HALFS, "transposed dK/dV tiles fit in LDS");
-  if (half == 0) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int off = (32 * db + l32) * LT + 8 * g + 4 * hi;
-        st64(tt + strip * TS + off, u32x2{pack2<E>(dkacc[db][4 * g], dkacc[db][4 * g + 1]),
-                                          pack2<E>(dkacc[db][4 * g + 2], dkacc[db][4 * g + 3])});
-        st64(tt + (NS + strip) * TS + off, u32x2{pack2<E>(dvacc[db][4 * g], dvacc[db][4 * g + 1]),
-                                                 pack2<E>(dvacc[db][4 * g + 2], dvacc[db][4 * g + 3])});
-      }
-  }
-  __syncthreads();
-  // Unit u = (pass, wave, lane group): tensor u >> 7, strip (u >> 5) & 3, 16-key block
-  // (u >> 4) & 1, 8-d chunk u & 15. Source lane s = 4 e + m of the group reads row d0 + e at keys
-  // 16 kb + 4 m; destination lane j receives d0 .. d0 + 3 of key 16 kb + j.
-  const int e4 = src >> 2, m4 = src & 3;
-#pragma unroll
-  for (int pass = 0; pass < 8; ++pass) {
-    const int u = pass * 32 + wave * 4 + grp;
-    const int tensor = u >> 7, st = (u >> 5) & 3, kb = (u >> 4) & 1, dc = u & 15;
-    const lds_u16* base = tt + (tensor * NS + st) * TS + (8 * dc + e4) * LT + 16 * kb + 4 * m4;
-    const u32x2 x = ldtr(base), y = ldtr(base + 4 * LT);
-    const int key = k0 + 32 * st + 16 * kb + src;
-    if (key < doc_end) {
-      uint16_t* dst = (tensor ? dv_part : dk_part) + ((long)key * hq + h) * D + 8 * dc;
-      gstore16(dst, u32x4{x[0], x[1], y[0], y[1]});
+      for (int c = 0; c < 2; ++c)
+        gstore16(dst + 32 * db + 16 * c,
+                 pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3], x[8 * c + 4],
+                          x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]));
     }
-  }
+  };
+  if (half) finish(dvacc, dkacc, 1.f, dv_part);
+  else finish(dkacc, dvacc, scale, dk_part);
 }
 
 // --------------------------------------------------------------------------------------------
