@@ -69,14 +69,15 @@ __device__ __forceinline__ void bwd_kv_item(
   const int kw0 = k0 + 32 * strip;
   const int my_key = kw0 + l32;
 
-  {  // K and V tiles, row-major, rows clamped to the document
-    const int srow = tid >> 4, scol = 8 * (tid & 15);
+  // K and V tiles, row-major, rows clamped to the document: loaded here, stored to LDS once the
+  // first step pair's loads are in flight too (one memory round trip for the whole prologue).
+  u32x4 kvr[2 * (BK / 32)];
+  const int kv_srow = tid >> 4, kv_scol = 8 * (tid & 15);
 #pragma unroll
-    for (int i = 0; i < BK / 32; ++i) {
-      const long g = (long)min(k0 + srow + 32 * i, doc_end - 1) * kvrow + kvh * D + scol;
-      st128(smem + KV_OFF_K + (srow + 32 * i) * LD + scol, gload16(k + g));
-      st128(smem + KV_OFF_V + (srow + 32 * i) * LD + scol, gload16(v + g));
-    }
+  for (int i = 0; i < BK / 32; ++i) {
+    const long g = (long)min(k0 + kv_srow + 32 * i, doc_end - 1) * kvrow + kvh * D + kv_scol;
+    kvr[2 * i] = gload16(k + g);
+    kvr[2 * i + 1] = gload16(v + g);
   }
 
   const int n_steps = (doc_end - k0 + BQ - 1) / BQ;
@@ -122,9 +123,9 @@ __device__ __forceinline__ void bwd_kv_item(
       d += __shfl_xor(d, 4, 16);
       d += __shfl_xor(d, 2, 16);
       d += __shfl_xor(d, 1, 16);
-      if ((tid & 15) == 0) stat[stage][sh][1][s_row] = d;
+      if ((tid & 15) == 0) stat[stage][1][sh][s_row] = d;
     }
-    if (tid < 64) stat[stage][tid >> 5][0][tid & 31] = st_row < doc_end ? st_lse * kLog2e : INFINITY;
+    if (tid < 64) stat[stage][0][tid >> 5][tid & 31] = st_row < doc_end ? st_lse * kLog2e : INFINITY;
   };
 
   const int rm_read = perm32(l32) * LD + 8 * hi;                 // A rows = queries
@@ -143,6 +144,11 @@ __device__ __forceinline__ void bwd_kv_item(
 
   if (half) __builtin_amdgcn_s_setprio(1);  // see the forward kernel: issue ties between halves
   gload_pair(0);
+#pragma unroll
+  for (int i = 0; i < BK / 32; ++i) {
+    st128(smem + KV_OFF_K + (kv_srow + 32 * i) * LD + kv_scol, kvr[2 * i]);
+    st128(smem + KV_OFF_V + (kv_srow + 32 * i) * LD + kv_scol, kvr[2 * i + 1]);
+  }
   store_pair(0);
   __syncthreads();
   for (int p = 0; p < n_pairs; ++p) {
@@ -185,7 +191,7 @@ __device__ __forceinline__ void bwd_kv_item(
       VA_SCHED(kSchedMfma, 3);
       // register j <-> query qs0 + reg_row(j, hi); P overwrites S, dS overwrites dP.
       const lds_f32x4* st = reinterpret_cast<const lds_f32x4*>(
-          (__attribute__((address_space(3))) float*)&stat[stage][half][0][0]);
+          (__attribute__((address_space(3))) float*)&stat[stage][0][half][0]);
       // The dV / dK operands do not depend on the softmax: their first reads go out before it.
       auto opt = [&](int i) {  // MFMA i: c = i >> 3, db = (i >> 1) & 3, dV (i even) / dK (odd)
         return ldtr8(((i & 1) ? qs : dos) + tr_read + 16 * (i >> 3) * LD + 32 * ((i >> 1) & 3), LD);
@@ -202,7 +208,7 @@ __device__ __forceinline__ void bwd_kv_item(
           for (int g4 = 0; g4 < 2; ++g4) {
             const int r0 = 16 * c + 8 * hi + 4 * g4;
             const f32x4 l4 = st[r0 / 4];
-            const f32x4 d4 = st[(BQ + r0) / 4];
+            const f32x4 d4 = st[(2 * BQ + r0) / 4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int j = 8 * c + 4 * g4 + e;
@@ -289,7 +295,7 @@ __device__ __forceinline__ void bwd_q_item(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, uint16_t* __restrict__ dq, int n_tokens, int hq, int hkv,
-    float scale, float scale_log2) {
+    float scale, float scale_log2, float* stat_f) {
   using namespace bwd;
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & 0xffffff;
   const int kvh = h / (hq / hkv);
@@ -300,24 +306,6 @@ __device__ __forceinline__ void bwd_q_item(
   const int wq0 = q0 + 32 * strip;
   const int my_q = wq0 + l32;
   const bool q_valid = my_q < doc_end;
-
-  // Q and dO rows of this lane's query as B operands (k slots = d); lse and delta in-lane.
-  u32x4 qf[8], df[8];
-  float lse2, dlt;
-  {
-    const long g = (long)min(my_q, doc_end - 1) * qrow + h * D + 8 * hi;
-    float acc = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      qf[kk] = gload16(q + g + 16 * kk);
-      df[kk] = gload16(dout + g + 16 * kk);
-      const u32x4 o8 = gload16(out + g + 16 * kk);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) acc = E::dot2(o8[w], df[kk][w], acc);
-    }
-    dlt = sum_with_other_half(acc);
-    lse2 = q_valid ? lse[(long)h * n_tokens + my_q] * kLog2e : INFINITY;
-  }
 
   const int kv_end = min(q0 + QB, doc_end);
   const int n_tiles = (kv_end - doc_start + BT - 1) / BT;
@@ -341,6 +329,45 @@ __device__ __forceinline__ void bwd_q_item(
     for (int i = 0; i < 4; ++i) st128(smem + stage * Q_PAIR + i * ROWT + srow * LD + scol, sr[i]);
   };
 
+  gload_pair(0);  // in flight together with the Q / dO / O loads below
+
+  // Q and dO of the item's 128 queries: coalesced buffer loads (16 lanes per row, rows past the
+  // document end read as zeros), staged in LDS after the two K / V stages; O only for delta =
+  // rowsum(dO * O), reduced over the 16 lanes of a row. Each lane then reads its query's Q and
+  // dO rows as B operands (k slots = d), lse and delta from the 256-float stat area.
+  constexpr int QT_OFF = Q_HALFS;
+  static_assert(Q_HALFS + 2 * QB * LD <= HALFS, "Q / dO tiles of a q item fit in LDS");
+  static_assert(2 * QB <= 2 * 2 * 2 * BQ, "lse / delta of a q item fit in the stat area");
+  {
+    const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(h + 1) * D) * 2;
+    const brsrc rq = make_rsrc(q + (long)q0 * qrow, bytes);
+    const brsrc rd = make_rsrc(dout + (long)q0 * qrow, bytes);
+    const brsrc ro = make_rsrc(out + (long)q0 * qrow, bytes);
+    u32x4 xq[QB / 32], xd[QB / 32], xo[QB / 32];
+#pragma unroll
+    for (int i = 0; i < QB / 32; ++i) {
+      const int off = ((srow + 32 * i) * (int)qrow + h * D + scol) * 2;
+      xq[i] = bload16(rq, off);
+      xd[i] = bload16(rd, off);
+      xo[i] = bload16(ro, off);
+    }
+    if (tid < QB)
+      stat_f[tid] = q0 + tid < doc_end ? lse[(long)h * n_tokens + q0 + tid] * kLog2e : INFINITY;
+#pragma unroll
+    for (int i = 0; i < QB / 32; ++i) {
+      st128(smem + QT_OFF + (srow + 32 * i) * LD + scol, xq[i]);
+      st128(smem + QT_OFF + QB * LD + (srow + 32 * i) * LD + scol, xd[i]);
+      float d = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) d = E::dot2(xo[i][w], xd[i][w], d);
+      d += __shfl_xor(d, 8, 16);
+      d += __shfl_xor(d, 4, 16);
+      d += __shfl_xor(d, 2, 16);
+      d += __shfl_xor(d, 1, 16);
+      if ((tid & 15) == 0) stat_f[QB + srow + 32 * i] = d;
+    }
+  }
+
   // LDS read bases: K / V rows as A operands (rows = keys through perm32, k = d); K^T through
   // transposed reads with the column order that keeps output registers d-contiguous.
   const int ka_read = (2 * half) * ROWT + perm32(l32) * LD + 8 * hi;
@@ -353,14 +380,20 @@ __device__ __forceinline__ void bwd_q_item(
   for (int db = 0; db < 4; ++db) dqacc[db] = f32x16{};
 
   if (half) __builtin_amdgcn_s_setprio(1);  // see the forward kernel: issue ties between halves
-  gload_pair(0);
   store_pair(0);
+  __syncthreads();
+  u32x4 qf[8], df[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    qf[kk] = ld128(smem + QT_OFF + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
+    df[kk] = ld128(smem + QT_OFF + QB * LD + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
+  }
+  const float lse2 = stat_f[32 * strip + l32], dlt = stat_f[QB + 32 * strip + l32];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
     settle(qf[kk]);
     settle(df[kk]);
   }
-  __syncthreads();
   for (int p = 0; p < n_pairs; ++p) {
     const int stage = p & 1;
     if (p + 1 < n_pairs) gload_pair(p + 1);
@@ -416,13 +449,17 @@ __device__ __forceinline__ void bwd_q_item(
     __syncthreads();
   }
 
-  // Half 1 hands its partial dQ^T to half 0 (same lane order), which scales and writes it.
-  float* xq = reinterpret_cast<float*>((uint16_t*)smem);
+  // Half 1 hands its partial dQ^T to half 0 (16-byte chunks, same lane order), which scales and
+  // writes it.
+  lds_f32x4* xq = reinterpret_cast<lds_f32x4*>((__attribute__((address_space(3))) float*)(smem));
+  auto qslot = [&](int db, int j4) { return ((strip * 4 + db) * 4 + j4) * 64 + lane; };
   if (half == 1) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) xq[(strip * 64 + 16 * db + j) * 64 + lane] = dqacc[db][j];
+      for (int j4 = 0; j4 < 4; ++j4)
+        xq[qslot(db, j4)] = f32x4{dqacc[db][4 * j4], dqacc[db][4 * j4 + 1], dqacc[db][4 * j4 + 2],
+                                  dqacc[db][4 * j4 + 3]};
   }
   __syncthreads();
   if (half == 1 || !q_valid) return;
@@ -431,8 +468,11 @@ __device__ __forceinline__ void bwd_q_item(
   for (int db = 0; db < 4; ++db) {
     float x[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      x[j] = (dqacc[db][j] + xq[(strip * 64 + 16 * db + j) * 64 + lane]) * scale;
+    for (int j4 = 0; j4 < 4; ++j4) {
+      const f32x4 y = xq[qslot(db, j4)];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * j4 + e] = (dqacc[db][4 * j4 + e] + y[e]) * scale;
+    }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const int j0 = 8 * c;  // register j <-> d = 32 db + reg_row(j, hi)
@@ -452,7 +492,7 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     const int4* __restrict__ items, int n_tokens, int hq, int hkv, float scale,
     float scale_log2) {
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
-  __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][half][lse|del]
+  __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
   lds_u16* smem = (lds_u16*)smem_raw;
   const int4 it = items[blockIdx.x];
   if (it.x >= it.y) return;  // an empty slot of a device-built plan
@@ -460,7 +500,8 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,
                    scale, scale_log2);
   } else {
-    bwd_q_item<E>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale, scale_log2);
+    bwd_q_item<E>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale, scale_log2,
+                  &stat[0][0][0][0]);
   }
 }
 
