@@ -14,6 +14,8 @@
 // global loads are in flight while the current pair is computed, one barrier per pair. The
 // running maximum is exact, so the dominant probability of a peaky row is exactly 1 in the 16-bit
 // P operand. Rows past the document end are clamped to its last row (finite) and masked.
+#include <type_traits>
+
 #include "va_common.h"
 #include "va_kernels.h"
 
@@ -58,13 +60,7 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   const int my_q = wq0 + l32;
   const bool q_valid = my_q < doc_end;
 
-  // Q fragment: B operand of S^T = K Q^T (column = this lane's query, k slots = d).
-  u32x4 qf[8];
-  {
-    const uint16_t* qp = q + (long)min(my_q, doc_end - 1) * qrow + h * D + 8 * hi;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[kk] = gload16(qp + 16 * kk);
-  }
+  u32x4 qf[8];  // Q fragment: B operand of S^T = K Q^T (filled from LDS before the loop)
 
   const int kv_end = min(q0 + BM, doc_end);
   const int n_tiles = (kv_end - doc_start + BN - 1) / BN;
@@ -190,11 +186,28 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   // The two waves of a SIMD come from different halves; the younger one (half 1) would otherwise
   // lose every issue tie and finish each pair last, keeping the others at the barrier.
   if (half) __builtin_amdgcn_s_setprio(1);
-  gload_pair(0);
+  // Q of the item's 128 queries: coalesced buffer loads (16 lanes per row, rows past the document
+  // end read as zeros), staged through the second LDS stage, which is free until the loop stores
+  // the second tile pair. Each lane then reads its query's row as the B operand of S^T = K Q^T
+  // (column = this lane's query, k slots = d).
+  {
+    const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(h + 1) * D) * 2;
+    const brsrc rq = make_rsrc(q + (long)q0 * qrow, bytes);
+    u32x4 xq[BM / 32];
+#pragma unroll
+    for (int i = 0; i < BM / 32; ++i) xq[i] = bload16(rq, ((srow + 32 * i) * (int)qrow + h * D + scol) * 2);
+    gload_pair(0);
+#pragma unroll
+    for (int i = 0; i < BM / 32; ++i) st128(smem + PAIR + (srow + 32 * i) * LD + scol, xq[i]);
+  }
+  static_assert(BM * LD <= PAIR, "the Q tile fits in one stage");
   store_pair(0);
+  __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + PAIR + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
-  __syncthreads();
+  __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
   for (int p = 0; p < n_pairs; ++p) {
     const int stage = p & 1;
     if (p + 1 < n_pairs) gload_pair(p + 1);
@@ -205,36 +218,50 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     __syncthreads();
   }
 
-  // Merge the two halves through LDS: half 1 publishes (O, m, l) in its lane order, which is
-  // the same (query, d) order as the partner wave of half 0.
-  float* xo = reinterpret_cast<float*>(smem_raw);          // [strip][64 reg][64 lanes]
-  float* xs = xo + NS * 64 * 64;                            // [strip][2][64 lanes]
-  if (half == 1) {
+  // Merge the two halves through LDS (same lane order: the partner wave holds the same (query,
+  // d) registers). Each half finishes half of the d columns: half h sends its partial O of the
+  // other half's columns, 16-byte chunks, and both publish (m, l).
+  lds_f32x4* xo = reinterpret_cast<lds_f32x4*>((__attribute__((address_space(3))) float*)(smem_raw));
+  float* xs = reinterpret_cast<float*>(smem_raw) + NS * 2 * 2 * 4 * 64 * 4;  // [strip][half][m|l][lane]
+  static_assert((NS * 2 * 2 * 4 * 64 * 4 + NS * 2 * 2 * 64) * 4 <= 2 * PAIR * 2, "merge fits in LDS");
+  auto slot = [&](int dst_half, int db2, int j4) {
+    return (((strip * 2 + dst_half) * 2 + db2) * 4 + j4) * 64 + lane;
+  };
+  // Accumulator indices must be compile-time constants (a runtime index would move oacc to
+  // scratch memory): the half is a template constant in each branch.
+  auto merge = [&](auto half_c) {
+    constexpr int H = decltype(half_c)::value;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db2 = 0; db2 < 2; ++db2) {
+      const int db = 2 * (H ^ 1) + db2;  // the partner's columns
 #pragma unroll
-      for (int j = 0; j < 16; ++j) xo[(strip * 64 + 16 * db + j) * 64 + lane] = oacc[db][j];
-    xs[(strip * 2 + 0) * 64 + lane] = m_run;
-    xs[(strip * 2 + 1) * 64 + lane] = l_run;
-  }
-  __syncthreads();
-  if (half == 1) return;
-  const float m_b = xs[(strip * 2 + 0) * 64 + lane];
-  const float l_b = xs[(strip * 2 + 1) * 64 + lane];
-  const float m_tot = fmaxf(m_run, m_b);
-  const float m_use = m_tot == -INFINITY ? 0.f : m_tot;
-  const float sa = fast_exp2(m_run - m_use), sb = fast_exp2(m_b - m_use);
-  const float l_tot = sum_with_other_half(l_run * sa + l_b * sb);
-  if (q_valid) {
+      for (int j4 = 0; j4 < 4; ++j4)
+        xo[slot(H ^ 1, db2, j4)] = f32x4{oacc[db][4 * j4], oacc[db][4 * j4 + 1],
+                                         oacc[db][4 * j4 + 2], oacc[db][4 * j4 + 3]};
+    }
+    xs[((strip * 2 + H) * 2 + 0) * 64 + lane] = m_run;
+    xs[((strip * 2 + H) * 2 + 1) * 64 + lane] = l_run;
+    __syncthreads();
+    const float m_b = xs[((strip * 2 + (H ^ 1)) * 2 + 0) * 64 + lane];
+    const float l_b = xs[((strip * 2 + (H ^ 1)) * 2 + 1) * 64 + lane];
+    const float m_tot = fmaxf(m_run, m_b);
+    const float m_use = m_tot == -INFINITY ? 0.f : m_tot;
+    const float sa = fast_exp2(m_run - m_use), sb = fast_exp2(m_b - m_use);
+    const float l_tot = sum_with_other_half(l_run * sa + l_b * sb);
+    if (!q_valid) return;
     const float inv = 1.f / l_tot;
     const float ca = sa * inv, cb = sb * inv;
     uint16_t* op = o + (long)my_q * qrow + h * D;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db2 = 0; db2 < 2; ++db2) {
+      const int db = 2 * H + db2;
       float x[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        x[j] = oacc[db][j] * ca + xo[(strip * 64 + 16 * db + j) * 64 + lane] * cb;
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const f32x4 y = xo[slot(H, db2, j4)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[4 * j4 + e] = oacc[db][4 * j4 + e] * ca + y[e] * cb;
+      }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int j0 = 8 * c;
@@ -243,8 +270,10 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
         gstore16(op + 32 * db + 16 * c + 8 * hi, w);
       }
     }
-    if (hi == 0) lse[(long)h * n_tokens + my_q] = (m_tot + fast_log2(l_tot)) * kLn2;
-  }
+    if (H == 0 && hi == 0) lse[(long)h * n_tokens + my_q] = (m_tot + fast_log2(l_tot)) * kLn2;
+  };
+  if (half) merge(std::integral_constant<int, 1>{});
+  else merge(std::integral_constant<int, 0>{});
 }
 
 template <class E>
