@@ -119,10 +119,7 @@ __device__ __forceinline__ void bwd_kv_item(
       float d = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) d = E::dot2(oreg[sh][w], sreg[2 * sh + 1][w], d);
-      d += __shfl_xor(d, 8, 16);
-      d += __shfl_xor(d, 4, 16);
-      d += __shfl_xor(d, 2, 16);
-      d += __shfl_xor(d, 1, 16);
+      d = sum_rows16(d);
       if ((tid & 15) == 0) stat[stage][1][sh][s_row] = d;
     }
     if (tid < 64) stat[stage][0][tid >> 5][tid & 31] = st_row < doc_end ? st_lse * kLog2e : INFINITY;
@@ -360,10 +357,7 @@ __device__ __forceinline__ void bwd_q_item(
       float d = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) d = E::dot2(xo[i][w], xd[i][w], d);
-      d += __shfl_xor(d, 8, 16);
-      d += __shfl_xor(d, 4, 16);
-      d += __shfl_xor(d, 2, 16);
-      d += __shfl_xor(d, 1, 16);
+      d = sum_rows16(d);
       if ((tid & 15) == 0) stat_f[QB + srow + 32 * i] = d;
     }
   }

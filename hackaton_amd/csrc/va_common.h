@@ -123,6 +123,19 @@ __device__ inline float sum_with_other_half(float x) {
   swap_halves(x, r0, r1);
   return r0 + r1;
 }
+// Sum over each group of 16 lanes (a DPP row), the same value in all 16: four DPP adds (swap
+// within pairs, within quads, mirror within 8, mirror within 16) instead of LDS permutes.
+template <int kCtrl>
+__device__ inline float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+}
+__device__ inline float sum_rows16(float x) {
+  x += dpp_mov<0xb1>(x);   // quad_perm [1, 0, 3, 2]
+  x += dpp_mov<0x4e>(x);   // quad_perm [2, 3, 0, 1]
+  x += dpp_mov<0x141>(x);  // row_half_mirror
+  x += dpp_mov<0x140>(x);  // row_mirror
+  return x;
+}
 
 // ---------------------------------------------------------------------------------------------
 // 32x32x16 MFMA block layout (64 lanes, lane = 32 * hi + l32):
