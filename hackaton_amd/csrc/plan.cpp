@@ -72,6 +72,37 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
   return items;
 }
 
+// The dispatcher hands work-group i to XCD i mod kXcds, and each XCD has its own L2. The G query
+// heads of a GQA group read the same K/V tiles, so the G items of one (tile, kind, group) are
+// placed kXcds apart: they run on one XCD at about the same time and share its L2. Groups are
+// taken in list order (longest first), kXcds at a time, as the columns of a block of G rows.
+constexpr int kXcds = 8;
+
+std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
+  if (group <= 1) return v;
+  std::vector<std::vector<Item>> combos;
+  for (const Item& x : v) {
+    const Item* last = combos.empty() ? nullptr : &combos.back().front();
+    const int32_t h = x.d & 0xffffff, kind = x.d >> 24;
+    if (last != nullptr && (int32_t)combos.back().size() < group && last->a == x.a &&
+        last->b == x.b && last->c == x.c && (last->d >> 24) == kind &&
+        (last->d & 0xffffff) / group == h / group) {
+      combos.back().push_back(x);
+    } else {
+      combos.push_back({x});
+    }
+  }
+  std::vector<Item> out;
+  out.reserve(v.size());
+  for (size_t c0 = 0; c0 < combos.size(); c0 += kXcds) {
+    const size_t c1 = std::min(combos.size(), c0 + kXcds);
+    for (int32_t r = 0; r < group; ++r)
+      for (size_t c = c0; c < c1; ++c)
+        if (r < (int32_t)combos[c].size()) out.push_back(combos[c][r]);
+  }
+  return out;
+}
+
 int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
   int64_t n = 0;
   for (int32_t i = 0; i < n_docs; ++i) {
@@ -110,7 +141,7 @@ extern "C" int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t 
   if (n > capacity) return va::fail(VA_ECAPACITY, "plan needs %lld items, capacity %lld",
                                     (long long)n, (long long)capacity);
   if (n > 0 && items == nullptr) return va::fail(VA_EINVAL, "items is NULL");
-  const std::vector<Item> v = make_items(cu_seqlens, n_docs, hq, kind);
+  const std::vector<Item> v = xcd_order(make_items(cu_seqlens, n_docs, hq, kind), hq / hkv);
   for (size_t i = 0; i < v.size(); ++i) {
     items[4 * i + 0] = v[i].a;
     items[4 * i + 1] = v[i].b;

@@ -58,7 +58,10 @@ int32_t va_head_dim(void);
 /* ---- work plan (host only; no GPU call) ------------------------------------------------------
  * Work items for the forward (kind VA_PLAN_FWD: one per 128-query tile x query head) or the
  * backward (VA_PLAN_BWD: one per 128-key tile x query head for dK/dV and one per 128-query tile
- * x query head for dQ) over the documents of cu_seqlens, ordered longest first. Fully masked causal tiles and cross-document tiles never appear.
+ * x query head for dQ) over the documents of cu_seqlens, longest first. The G = Hq / Hkv items of
+ * one tile and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the
+ * heads sharing K/V run on one XCD and share its L2. Fully masked causal tiles and
+ * cross-document tiles never appear.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
 int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                  int64_t* n_items);

@@ -51,8 +51,27 @@ def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
     expected = {(q0, h) for s, e in zip(cu[:-1], cu[1:]) for q0 in range(s, e, 128)
                 for h in range(hq)}
     assert seen == expected and len(items) == len(expected)
-    # longest first: keys visited per tile never increase along the list
-    work = [min(q0 + 128, e) - s for q0, e, s, _ in items.tolist()]
+    check_xcd_order(items, hq, hkv, lambda q0, e, s, w: min(q0 + 128, e) - s)
+
+
+def check_xcd_order(items, hq, hkv, work_of):
+    """The G = Hq / Hkv items of one (tile, kind, GQA group) sit a constant stride apart, at most
+    8 (the XCD count: work-group i runs on XCD i mod 8, so they share one L2), and the groups
+    come longest first."""
+    g = hq // hkv
+    combos = {}
+    for pos, (a, e, s, w) in enumerate(items.tolist()):
+        key = (a, e, s, w >> 24, (w & 0xFFFFFF) // g)
+        combos.setdefault(key, []).append((pos, work_of(a, e, s, w)))
+    firsts = []
+    for key, entries in combos.items():
+        assert len(entries) == g
+        pos = [p for p, _ in entries]
+        steps = {b - a for a, b in zip(pos, pos[1:])}
+        assert len(steps) <= 1 and all(0 < x <= 8 for x in steps), (key, pos)
+        assert len({w for _, w in entries}) == 1
+        firsts.append((pos[0], entries[0][1]))
+    work = [w for _, w in sorted(firsts)]
     assert work == sorted(work, reverse=True)
 
 
@@ -73,6 +92,12 @@ def test_backward_plan_covers_every_key_and_query_tile_once(lengths):
                 for h in range(hq)}
     assert kv_seen == expected and q_seen == expected
     assert len(items) == 2 * len(expected)
+
+    def work(a, e, s, w):  # the planner's measure: MFMAs per wave per step pair
+        if w >> 24 == 0:
+            return ((e - a + 31) // 32 + 1) // 2 * 32
+        return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24
+    check_xcd_order(items, hq, hkv, work)
 
 
 def test_plan_rejects_bad_cu_seqlens():
