@@ -253,6 +253,9 @@ __device__ __forceinline__ void bwd_kv_item(
       (__attribute__((address_space(3))) float*)(smem));
   auto slot = [&](int tensor, int db, int j4) { return ((tensor * NS + strip) * 16 + 4 * db + j4) * 64 + lane; };
   static_assert(2 * NS * 16 * 64 * 16 <= HALFS * 2, "dK/dV exchange fits in LDS");
+  // The finished 32 x 128 tile goes out through this wave's own exchange slot (read just before,
+  // by this wave only) as a row-major LDS tile, so that each 16-byte global store instruction
+  // writes 4 whole rows instead of 32-byte pieces of 32 rows.
   auto finish = [&](f32x16(&mine)[4], const f32x16(&other)[4], float mul, uint16_t* part) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -261,8 +264,7 @@ __device__ __forceinline__ void bwd_kv_item(
         xs[slot(half ^ 1, db, j4)] = f32x4{other[db][4 * j4], other[db][4 * j4 + 1],
                                            other[db][4 * j4 + 2], other[db][4 * j4 + 3]};
     __syncthreads();
-    if (my_key >= doc_end) return;
-    uint16_t* dst = part + ((long)my_key * hq + h) * D + 8 * hi;
+    u32x4 w[8];  // chunk 2 db + c: d = 32 db + 16 c + 8 hi + 0..7 of key kw0 + l32
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       float x[16];
@@ -274,10 +276,11 @@ __device__ __forceinline__ void bwd_kv_item(
       }
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        gstore16(dst + 32 * db + 16 * c,
-                 pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3], x[8 * c + 4],
-                          x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]));
+        w[2 * db + c] = pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3],
+                                 x[8 * c + 4], x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]);
     }
+    store_rows32<16>(reinterpret_cast<lds_u16*>(&xs[slot(half, 0, 0) - lane]), w, lane,
+                    [&](int r) { return part + ((long)(kw0 + r) * hq + h) * D; }, doc_end - kw0);
   };
   if (half) finish(dvacc, dkacc, 1.f, dv_part);
   else finish(dkacc, dvacc, scale, dk_part);
@@ -302,7 +305,6 @@ __device__ __forceinline__ void bwd_q_item(
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
   const int wq0 = q0 + 32 * strip;
   const int my_q = wq0 + l32;
-  const bool q_valid = my_q < doc_end;
 
   const int kv_end = min(q0 + QB, doc_end);
   const int n_tiles = (kv_end - doc_start + BT - 1) / BT;
@@ -443,38 +445,48 @@ __device__ __forceinline__ void bwd_q_item(
     __syncthreads();
   }
 
-  // Half 1 hands its partial dQ^T to half 0 (16-byte chunks, same lane order), which scales and
-  // writes it.
+  // The halves swap partial dQ^T columns (16-byte chunks, same lane order): half h finishes
+  // d in [64 h, 64 h + 64) of its strip's 32 queries and writes them as whole 128-byte row halves
+  // through its own exchange slot as an LDS row tile. The half is a template constant in each
+  // branch, so the accumulator indices are compile-time (a runtime index would move them to
+  // scratch memory).
   lds_f32x4* xq = reinterpret_cast<lds_f32x4*>((__attribute__((address_space(3))) float*)(smem));
-  auto qslot = [&](int db, int j4) { return ((strip * 4 + db) * 4 + j4) * 64 + lane; };
-  if (half == 1) {
+  auto qslot = [&](int dst_half, int db2, int j4) {
+    return (((dst_half * NS + strip) * 2 + db2) * 4 + j4) * 64 + lane;
+  };
+  auto finish = [&](auto half_c) {
+    constexpr int H = decltype(half_c)::value;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db2 = 0; db2 < 2; ++db2)
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4)
-        xq[qslot(db, j4)] = f32x4{dqacc[db][4 * j4], dqacc[db][4 * j4 + 1], dqacc[db][4 * j4 + 2],
-                                  dqacc[db][4 * j4 + 3]};
-  }
-  __syncthreads();
-  if (half == 1 || !q_valid) return;
-  uint16_t* dqp = dq + (long)my_q * qrow + h * D;
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const int db = 2 * (H ^ 1) + db2;
+        xq[qslot(H ^ 1, db2, j4)] = f32x4{dqacc[db][4 * j4], dqacc[db][4 * j4 + 1],
+                                          dqacc[db][4 * j4 + 2], dqacc[db][4 * j4 + 3]};
+      }
+    __syncthreads();
+    u32x4 w[4];  // chunk 2 db2 + c: d = 64 H + 32 db2 + 16 c + 8 hi + 0..7 of query wq0 + l32
 #pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    float x[16];
+    for (int db2 = 0; db2 < 2; ++db2) {
+      const int db = 2 * H + db2;
+      float x[16];
 #pragma unroll
-    for (int j4 = 0; j4 < 4; ++j4) {
-      const f32x4 y = xq[qslot(db, j4)];
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const f32x4 y = xq[qslot(H, db2, j4)];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[4 * j4 + e] = (dqacc[db][4 * j4 + e] + y[e]) * scale;
+        for (int e = 0; e < 4; ++e) x[4 * j4 + e] = (dqacc[db][4 * j4 + e] + y[e]) * scale;
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        w[2 * db2 + c] = pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3],
+                                  x[8 * c + 4], x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]);
     }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int j0 = 8 * c;  // register j <-> d = 32 db + reg_row(j, hi)
-      gstore16(dqp + 32 * db + 16 * c + 8 * hi,
-               pack8<E>(x[j0], x[j0 + 1], x[j0 + 2], x[j0 + 3], x[j0 + 4], x[j0 + 5], x[j0 + 6],
-                        x[j0 + 7]));
-    }
-  }
+    store_rows32<8>(reinterpret_cast<lds_u16*>(&xq[qslot(H, 0, 0) - lane]), w, lane,
+                    [&](int r) { return dq + (long)(wq0 + r) * qrow + h * D + 64 * H; },
+                    doc_end - wq0);
+  };
+  if (half) finish(std::integral_constant<int, 1>{});
+  else finish(std::integral_constant<int, 0>{});
 }
 
 template <class E>

@@ -248,10 +248,9 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     const float m_use = m_tot == -INFINITY ? 0.f : m_tot;
     const float sa = fast_exp2(m_run - m_use), sb = fast_exp2(m_b - m_use);
     const float l_tot = sum_with_other_half(l_run * sa + l_b * sb);
-    if (!q_valid) return;
     const float inv = 1.f / l_tot;
     const float ca = sa * inv, cb = sb * inv;
-    uint16_t* op = o + (long)my_q * qrow + h * D;
+    u32x4 w[4];  // chunk 2 db2 + c: d = 64 H + 32 db2 + 16 c + 8 hi + 0..7 of query wq0 + l32
 #pragma unroll
     for (int db2 = 0; db2 < 2; ++db2) {
       const int db = 2 * H + db2;
@@ -263,13 +262,16 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
         for (int e = 0; e < 4; ++e) x[4 * j4 + e] = oacc[db][4 * j4 + e] * ca + y[e] * cb;
       }
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int j0 = 8 * c;
-        const u32x4 w = pack8<E>(x[j0], x[j0 + 1], x[j0 + 2], x[j0 + 3], x[j0 + 4], x[j0 + 5],
-                                 x[j0 + 6], x[j0 + 7]);
-        gstore16(op + 32 * db + 16 * c + 8 * hi, w);
-      }
+      for (int c = 0; c < 2; ++c)
+        w[2 * db2 + c] = pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3],
+                                  x[8 * c + 4], x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]);
     }
+    // Whole 128-byte row halves through this wave's own exchange slot (read above by this wave
+    // only) as an LDS row tile.
+    store_rows32<8>(reinterpret_cast<lds_u16*>(&xo[slot(H, 0, 0) - lane]), w, lane,
+                    [&](int r) { return o + (long)(wq0 + r) * qrow + h * D + 64 * H; },
+                    doc_end - wq0);
+    if (!q_valid) return;
     if (H == 0 && hi == 0) lse[(long)h * n_tokens + my_q] = (m_tot + fast_log2(l_tot)) * kLn2;
   };
   if (half) merge(std::integral_constant<int, 1>{});

@@ -272,6 +272,28 @@ __device__ __host__ inline int swz16(int r) {
 }
 __device__ inline void gstore16(uint16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// Stores a wave's 32 rows x 8C columns (16-bit) through an LDS row tile (32 x (8C + 8) halfs,
+// used by this wave only): lane (l32, hi) holds in w[i] the columns 8 (2 i + hi) + 0..7 of row
+// l32. Each global store instruction then writes 64 / C whole rows of 16 C bytes (C lanes x 16
+// bytes per row) instead of 32-byte pieces of 32 rows. Rows >= n_rows are skipped; row_ptr(r)
+// is the global address of column 0 of row r.
+template <int C, class RowPtr>
+__device__ inline void store_rows32(lds_u16* tile, const u32x4 (&w)[C / 2], int lane,
+                                    RowPtr row_ptr, int n_rows) {
+  static_assert(C == 8 || C == 16, "64 or 128 columns");
+  constexpr int LT = 8 * C + 8;
+  const int l32 = lane & 31, hi = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < C / 2; ++i) st128(tile + l32 * LT + 8 * (2 * i + hi), w[i]);
+  const int r0 = lane / C, col = 8 * (lane % C);
+#pragma unroll
+  for (int i = 0; i < C / 2; ++i) {
+    const int r = (64 / C) * i + r0;
+    const u32x4 v = ld128(tile + r * LT + col);
+    if (r < n_rows) gstore16(row_ptr(r) + col, v);
+  }
+}
+
 __device__ inline uint16_t half_of(const u32x4& v, int e) {
   const uint32_t w = v[e >> 1];
   return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
