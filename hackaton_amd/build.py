@@ -17,11 +17,10 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "rope.hip", "plan_device.hip", "api.cpp", "plan.cpp"]
 ARCH = os.environ.get("VA_OFFLOAD_ARCH", "gfx950")
 
-# -munsafe-fp-atomics: hardware global_atomic_add_f32 for the fp32 dQ/dK/dV accumulators.
 # -packed-fp32-ops off: no packed fp32 VALU instructions are generated.
 # -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs, so the softmax rescale of O and the
 #   reads of S need no accumulation-register moves.
-HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-munsafe-fp-atomics",
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-mllvm", "-amdgpu-mfma-vgpr-form",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
              "-Wno-unused-function"]

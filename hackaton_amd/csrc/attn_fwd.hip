@@ -4,16 +4,18 @@
 // query head, run by 8 waves in two halves. Half h (waves 4h .. 4h + 3) processes the key tiles
 // t = h, h + 2, h + 4, ... (64 keys each) for the 4 query strips, so two waves share each SIMD:
 // one wave's MFMAs overlap the other's softmax, LDS waits and barrier skew, and the key range of
-// the work item is split in two. At the end half 1 hands its unnormalised (O, m, l) to half 0
-// through LDS and half 0 merges, normalises and writes O and the log-sum-exp.
+// the work item is split in two. At the end the halves swap their unnormalised partial O through
+// LDS and publish (m, l); each half finishes 64 of the 128 columns, half 0 also the log-sum-exp.
 //
-// Per wave: Q stays in registers as the MFMA B operand; S^T = K Q^T (v_mfma_f32_32x32x16) puts
-// one query per lane, so the online softmax is in-lane plus one v_permlane32_swap; O^T += V^T P^T
-// reads V^T straight from the row-major tile with ds_read_b64_tr_b16. K/V tiles stream through
-// two LDS stages of tile pairs (plain row-major copies, row stride 136 halfs); the next pair's
-// global loads are in flight while the current pair is computed, one barrier per pair. The
-// running maximum is exact, so the dominant probability of a peaky row is exactly 1 in the 16-bit
-// P operand. Rows past the document end are clamped to its last row (finite) and masked.
+// Per wave: Q (staged once through LDS from coalesced row loads) stays in registers as the MFMA B
+// operand; S^T = K Q^T (v_mfma_f32_32x32x16) puts one query per lane, so the online softmax is
+// in-lane plus one v_permlane32_swap; O^T += V^T P^T reads V^T straight from the row-major tile
+// with ds_read_b64_tr_b16. K/V tiles stream through two LDS stages of tile pairs (plain row-major
+// copies, row stride 136 halfs); the next pair's global loads are in flight while the current
+// pair is computed, one barrier per pair. Loads are buffer loads bounded at the document end: rows
+// past it read as zeros (masked keys, zero P). The running maximum moves lazily (only when a tile
+// exceeds it by more than 2^8), so P stays below 256 and the O / l rescale is skipped on most
+// tiles.
 #include <type_traits>
 
 #include "va_common.h"
