@@ -20,8 +20,10 @@ ARCH = os.environ.get("VA_OFFLOAD_ARCH", "gfx950")
 # -packed-fp32-ops off: no packed fp32 VALU instructions are generated.
 # -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs, so the softmax rescale of O and the
 #   reads of S need no accumulation-register moves.
+# -amdgpu-kernarg-preload-count: the first kernel arguments arrive in SGPRs at launch instead of
+#   through a scalar load, one memory round trip less before a work-group's first loads.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
-             "-mllvm", "-amdgpu-mfma-vgpr-form",
+             "-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
              "-Wno-unused-function"]
 

@@ -490,13 +490,14 @@ __device__ __forceinline__ void bwd_q_item(
 }
 
 template <class E>
+// Arguments in the order the work-group needs them: the first 14 dwords are preloaded into
+// SGPRs at launch (-amdgpu-kernarg-preload-count), so the work item's load starts at once.
 __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint16_t* __restrict__ out,
-    const uint16_t* __restrict__ dout, const float* __restrict__ lse, uint16_t* __restrict__ dq,
-    uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part,
-    const int4* __restrict__ items, int n_tokens, int hq, int hkv, float scale,
-    float scale_log2) {
+    const int4* __restrict__ items, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, int hq, int hkv,
+    const float* __restrict__ lse, uint16_t* __restrict__ dq, uint16_t* __restrict__ dk_part,
+    uint16_t* __restrict__ dv_part, int n_tokens, float scale, float scale_log2) {
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
   lds_u16* smem = (lds_u16*)smem_raw;
@@ -558,10 +559,10 @@ template <class E>
 static hipError_t launch_bwd_main_t(const BwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
   hipLaunchKernelGGL((bwd_kernel<E>), dim3((unsigned)a.n_items), dim3(bwd::NT), 0, a.stream,
-                     (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
-                     (const uint16_t*)a.out, (const uint16_t*)a.dout, a.lse, (uint16_t*)a.dq,
-                     (uint16_t*)a.dk_part, (uint16_t*)a.dv_part, (const int4*)a.items,
-                     (int)a.n_tokens, a.hq, a.hkv, a.scale, a.scale * kLog2e);
+                     (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
+                     (const uint16_t*)a.v, (const uint16_t*)a.out, (const uint16_t*)a.dout, a.hq,
+                     a.hkv, a.lse, (uint16_t*)a.dq, (uint16_t*)a.dk_part, (uint16_t*)a.dv_part,
+                     (int)a.n_tokens, a.scale, a.scale * kLog2e);
   return hipGetLastError();
 }
 

@@ -40,10 +40,12 @@ static_assert(BM == kFwdBlockM, "the plan's query tile");
 }  // namespace fwd
 
 template <class E>
+// Arguments in the order the work-group needs them: the first 14 dwords are preloaded into
+// SGPRs at launch (-amdgpu-kernarg-preload-count), so the work item's load starts at once.
 __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
-    const int4* __restrict__ items, int n_tokens, int hq, int hkv, float scale_log2) {
+    const int4* __restrict__ items, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int hq, int hkv,
+    uint16_t* __restrict__ o, float* __restrict__ lse, int n_tokens, float scale_log2) {
   using namespace fwd;
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[2 * PAIR];
   lds_u16* smem = (lds_u16*)smem_raw;
@@ -284,8 +286,8 @@ template <class E>
 static hipError_t launch_fwd_t(const FwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
   hipLaunchKernelGGL((fwd_kernel<E>), dim3((unsigned)a.n_items), dim3(fwd::NT), 0, a.stream,
-                     (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
-                     (uint16_t*)a.out, a.lse, (const int4*)a.items, (int)a.n_tokens, a.hq, a.hkv,
+                     (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
+                     (const uint16_t*)a.v, a.hq, a.hkv, (uint16_t*)a.out, a.lse, (int)a.n_tokens,
                      a.scale * kLog2e);
   return hipGetLastError();
 }
