@@ -30,12 +30,11 @@ constexpr int NW = 2 * NS;      // waves: two halves over the key tiles
 constexpr int NT = NW * 64;
 constexpr int BN = 64;          // keys per tile
 constexpr int D = kHeadDim;
-constexpr int LD = D + 8;       // LDS row stride (halfs) of the K and V tiles
-constexpr int TILE = BN * LD;   // halfs per K or V tile
+constexpr int TILE = BN * D;    // halfs per K or V tile: 256-byte rows, chunks swizzled by swz16
 constexpr int PAIR = 4 * TILE;  // K0, V0, K1, V1 of one tile pair
-constexpr int LPT = 4 * BN * 16 / NT;  // 16-byte staging chunks per thread per pair
+constexpr int LQ = D + 8;       // LDS row stride (halfs) of the Q tile, staged once
 constexpr float kRescaleLog2 = 8.f;     // largest P before the running maximum must move
-static_assert(LPT * NT == 4 * BN * 16, "pair staging split");
+static_assert(NT == 512 && BN == 64, "pair copy map: 2 groups of 4 rows per wave and tile");
 static_assert(BM == kFwdBlockM, "the plan's query tile");
 }  // namespace fwd
 
@@ -70,37 +69,57 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   const int n_tiles = (kv_end - doc_start + BN - 1) / BN;
   const int n_pairs = (n_tiles + 1) / 2;
 
-  // Staging of one tile pair: chunk i of this thread is tile (i >> 2), tensor ((i >> 1) & 1),
-  // row (tid >> 4) + 32 (i & 1), 16-byte column (tid & 15). Buffer loads bounded at the document
-  // end: rows past it read as zeros (masked keys, zero P).
-  const int srow = tid >> 4, scol = 8 * (tid & 15);
-  int voff[4];
+  // Copy of one tile pair straight from HBM into LDS (buffer loads that write LDS, no staging
+  // registers): wave w moves rows 4 (2 w + j) .. + 3 of each tile (K0, V0, K1, V1), one
+  // instruction per 4 rows; lane i lands in chunk slot i & 15 of row i >> 4 of the group, so it
+  // fetches logical chunk (i & 15) ^ swz16(row). Loads are bounded at the document end: rows past
+  // it read as zeros (masked keys, zero P).
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int srow = tid >> 4, scol = 8 * (tid & 15);  // Q staging: 16 lanes per 256-byte row
+  int coff[2];  // [j], bytes from the tile's first row
 #pragma unroll
-  for (int i = 0; i < 4; ++i) voff[i] = (((i >> 1) * BN + srow + 32 * (i & 1)) * (int)kvrow + scol) * 2;
-  u32x4 sr[LPT];
-  auto gload_pair = [&](int p) {
-    const int row0 = doc_start + 2 * p * BN;
-    const long base = (long)row0 * kvrow + kvh * D;
-    const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
-    const brsrc rk = make_rsrc(k + base, bytes), rv = make_rsrc(v + base, bytes);
+  for (int j = 0; j < 2; ++j) {
+    const int r = 4 * (2 * wave + j) + (lane >> 4);
+    coff[j] = (r * (int)kvrow + 8 * ((lane & 15) ^ swz16(r))) * 2;
+  }
+  // All 8 copies of a wave are issued together at the start of a pair: the wave then stalls on
+  // the memory queue once (the copies move 64 KB per pair into the CU), which costs less than
+  // stalling between MFMAs. Copy (t, x, j): tile t of the pair, tensor x (K, V), row group j.
+  auto copy_pair = [&](int p, int stage) {
+    const uint32_t dst = lds_addr(smem + stage * PAIR + 8 * wv * D);
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int c = ((i >> 2) << 1) | (i & 1);
-      sr[i] = bload16(((i >> 1) & 1) ? rv : rk, voff[c]);
-    }
-  };
-  auto store_pair = [&](int stage) {
-    lds_u16* base = smem + stage * PAIR + srow * LD + scol;
+    for (int t = 0; t < 2; ++t) {
+      const int row0 = doc_start + (2 * p + t) * BN;
+      const long base = (long)row0 * kvrow + kvh * D;
+      const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
+      const u32x4 r[2] = {make_rsrc4(k + base, bytes), make_rsrc4(v + base, bytes)};
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      st128(base + ((i >> 2) * 2 + ((i >> 1) & 1)) * TILE + 32 * (i & 1) * LD, sr[i]);
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          dma16_opaque(r[x], dst + ((2 * t + x) * TILE + 4 * j * D) * 2, coff[j]);
     }
   };
 
-  // Per-lane LDS read bases (halfs) inside this half's K / V tile of a stage.
-  const int kread = 2 * half * TILE + perm32(l32) * LD + 8 * hi;     // K rows, k = d
-  const int vread = (2 * half + 1) * TILE + (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1)
-                    + 4 * ((((src & 3) & 1) << 1) | ((src & 3) >> 1));  // V^T via tr reads
+  // Per-lane LDS read offsets (halfs) inside a tile. K (A operand of S^T): row perm32(l32)
+  // (+32 b), logical chunk 2 kk + hi. V^T (transposed reads): row 8 hi + 2 (src >> 2) + e
+  // (+16 c + 32 b), logical column 16 (grp & 1) + 32 db + 4 sg, sg the column order that keeps
+  // output registers d-contiguous. Adding 16 c + 32 b to a row keeps its swizzle.
+  int koff[8], toff[4][2];
+  {
+    const int r = perm32(l32), f = swz16(r);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) koff[kk] = r * D + 8 * ((2 * kk + hi) ^ f);
+    const int sg = (((src & 3) & 1) << 1) | ((src & 3) >> 1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int rr = 8 * hi + 2 * (src >> 2) + e;
+        const int lc = 2 * (grp & 1) + 4 * db + (sg >> 1);
+        toff[db][e] = rr * D + 8 * (lc ^ swz16(rr)) + 4 * (sg & 1);
+      }
+  }
 
   f32x16 oacc[4];
 #pragma unroll
@@ -110,17 +129,17 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   // One 64-key tile for this wave: S^T, mask, online softmax, O^T += V^T P^T.
   auto tile = [&](int stage, int t) {
     const int kv0 = doc_start + t * BN;
-    const lds_u16* kb = smem + stage * PAIR + kread;
+    const lds_u16* kb = smem + stage * PAIR + 2 * half * TILE;
     // S^T: 16 MFMAs over (kk, b), each K operand read from LDS 4 MFMAs ahead of its use.
     f32x16 s[2] = {f32x16{}, f32x16{}};
     u32x4 ka[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ka[i] = ld128(kb + 32 * (i & 1) * LD + 16 * (i >> 1));
+    for (int i = 0; i < 4; ++i) ka[i] = ld128(kb + koff[i >> 1] + 32 * (i & 1) * D);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int kk = i >> 1, b = i & 1;
       s[b] = E::mfma(ka[i & 3], qf[kk], s[b]);
-      if (i + 4 < 16) ka[i & 3] = ld128(kb + 32 * ((i + 4) & 1) * LD + 16 * ((i + 4) >> 1));
+      if (i + 4 < 16) ka[i & 3] = ld128(kb + koff[(i + 4) >> 1] + 32 * ((i + 4) & 1) * D);
     }
     VA_SCHED(kSchedDsRead, 4);
 #pragma unroll
@@ -130,14 +149,16 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     }
     VA_SCHED(kSchedMfma, 4);
     // The first V^T operands of O^T += V^T P^T, read while the softmax runs.
-    const lds_u16* vb = smem + stage * PAIR + vread;
-    auto v_addr = [&](int i) {  // i = (b, c, db) in MFMA order
+    const lds_u16* vb = smem + stage * PAIR + (2 * half + 1) * TILE;
+    auto v_read = [&](int i) {  // i = (b, c, db) in MFMA order
       const int b = i >> 3, c = (i >> 2) & 1, db = i & 3;
-      return vb + (32 * b + 16 * c) * LD + 32 * db;
+      const lds_u16* p = vb + (32 * b + 16 * c) * D;
+      const u32x2 x = ldtr(p + toff[db][0]), y = ldtr(p + toff[db][1]);
+      return u32x4{x[0], x[1], y[0], y[1]};
     };
     u32x4 va[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) va[i] = ldtr8(v_addr(i), LD);
+    for (int i = 0; i < 4; ++i) va[i] = v_read(i);
     if (kv0 + BN - 1 > wq0) {  // the tile crosses this strip's diagonal: key > query -> -inf
       const int lim = my_q - kv0;
 #pragma unroll
@@ -183,7 +204,7 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     for (int i = 0; i < 16; ++i) {
       const int b = i >> 3, c = (i >> 2) & 1, db = i & 3;
       oacc[db] = E::mfma(va[i & 3], pf[b][c], oacc[db]);
-      if (i + 4 < 16) va[i & 3] = ldtr8(v_addr(i + 4), LD);
+      if (i + 4 < 16) va[i & 3] = v_read(i + 4);
     }
   };
 
@@ -200,25 +221,25 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     u32x4 xq[BM / 32];
 #pragma unroll
     for (int i = 0; i < BM / 32; ++i) xq[i] = bload16(rq, ((srow + 32 * i) * (int)qrow + h * D + scol) * 2);
-    gload_pair(0);
+    copy_pair(0, 0);
 #pragma unroll
-    for (int i = 0; i < BM / 32; ++i) st128(smem + PAIR + (srow + 32 * i) * LD + scol, xq[i]);
+    for (int i = 0; i < BM / 32; ++i) st128(smem + PAIR + (srow + 32 * i) * LQ + scol, xq[i]);
   }
-  static_assert(BM * LD <= PAIR, "the Q tile fits in one stage");
-  store_pair(0);
+  static_assert(BM * LQ <= PAIR, "the Q tile fits in one stage");
+  wait_vmcnt<0>();
   __syncthreads();
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + PAIR + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
+  for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + PAIR + (32 * strip + l32) * LQ + 16 * kk + 8 * hi);
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
   __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
   for (int p = 0; p < n_pairs; ++p) {
     const int stage = p & 1;
-    if (p + 1 < n_pairs) gload_pair(p + 1);
+    if (p + 1 < n_pairs) copy_pair(p + 1, stage ^ 1);
     const int t = 2 * p + half;
     // Tiles entirely past this strip's diagonal are skipped (their P would be all zero).
     if (t < n_tiles && doc_start + t * BN <= wq0 + 31) tile(stage, t);
-    if (p + 1 < n_pairs) store_pair(stage ^ 1);
+    wait_vmcnt<0>();  // this wave's copies of the next pair have landed in LDS
     __syncthreads();
   }
 

@@ -255,6 +255,25 @@ __device__ inline void dma16(brsrc r, lds_u16* dst, int byte_off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
                                            byte_off, 0, 0, 0);
 }
+// The same copy issued as inline assembly, invisible to the compiler's wait-count tracking: the
+// compiler treats an LDS-writing buffer load as a possible writer of every later transposed LDS
+// read and waits for it to land before each one, which would serialise the copy of the next tile
+// with the MFMAs of the current one. Callers order the copies themselves: wait_vmcnt and a
+// barrier before any wave reads the destination, and the destination not read by any wave since
+// the last barrier. `rsrc` is a buffer descriptor in SGPRs (make_rsrc4), `lds_byte` the
+// wave-uniform LDS byte address of lane 0's 16 bytes.
+__device__ inline void dma16_opaque(u32x4 rsrc, uint32_t lds_byte, int byte_off) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_byte), "v"(byte_off), "s"(rsrc)
+               : "m0");
+}
+__device__ inline u32x4 make_rsrc4(const void* base, long bytes) {
+  const unsigned long long a = (unsigned long long)base;
+  const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffffL ? 0x7fffffff : (int)bytes);
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, (uint32_t)n, 0x00020000u};
+}
+__device__ inline uint32_t lds_addr(const lds_u16* p) { return (uint32_t)(uintptr_t)p; }
 // s_waitcnt vmcnt(N): at most N vector-memory operations of this wave still outstanding.
 template <int N>
 __device__ inline void wait_vmcnt() {
