@@ -70,23 +70,27 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   const int n_pairs = (n_tiles + 1) / 2;
 
   // Copy of one tile pair straight from HBM into LDS (buffer loads that write LDS, no staging
-  // registers): wave w moves rows 4 (2 w + j) .. + 3 of each tile (K0, V0, K1, V1), one
-  // instruction per 4 rows; lane i lands in chunk slot i & 15 of row i >> 4 of the group, so it
-  // fetches logical chunk (i & 15) ^ swz16(row). Loads are bounded at the document end: rows past
-  // it read as zeros (masked keys, zero P).
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  // registers): one instruction moves 4 rows (a row group) of a tile (K0, V0, K1, V1); lane i
+  // lands in chunk slot i & 15 of row i >> 4 of the group, so it fetches logical chunk
+  // (i & 15) ^ swz16(row). Loads are bounded at the document end: rows past it read as zeros
+  // (masked keys, zero P).
   const int srow = tid >> 4, scol = 8 * (tid & 15);  // Q staging: 16 lanes per 256-byte row
-  int coff[2];  // [j], bytes from the tile's first row
+  // Only the waves of half 1 copy: a copy instruction stalls its wave on the memory queue until
+  // the CU takes it (64 KB per pair enter the CU at ~80 B/clk), and with one copying wave per
+  // SIMD the other one starts its MFMAs at once, so the two run out of phase. Wave (1, s) moves
+  // row groups g = 2 s + j and 2 (s + 4) + j (j = 0, 1) of each tile, 4 rows per instruction.
+  const int ws = __builtin_amdgcn_readfirstlane(strip);
+  int coff[4];  // [jj]: bytes from the tile's first row, row group 2 (s + 4 (jj >> 1)) + (jj & 1)
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 4 * (2 * wave + j) + (lane >> 4);
-    coff[j] = (r * (int)kvrow + 8 * ((lane & 15) ^ swz16(r))) * 2;
+  for (int jj = 0; jj < 4; ++jj) {
+    const int r = 4 * (2 * (strip + 4 * (jj >> 1)) + (jj & 1)) + (lane >> 4);
+    coff[jj] = (r * (int)kvrow + 8 * ((lane & 15) ^ swz16(r))) * 2;
   }
-  // All 8 copies of a wave are issued together at the start of a pair: the wave then stalls on
-  // the memory queue once (the copies move 64 KB per pair into the CU), which costs less than
-  // stalling between MFMAs. Copy (t, x, j): tile t of the pair, tensor x (K, V), row group j.
+  // All 16 copies of a wave are issued together at the start of a pair (stalling between MFMAs
+  // costs more). Copy (t, x, jj): tile t of the pair, tensor x (K, V), row group jj.
   auto copy_pair = [&](int p, int stage) {
-    const uint32_t dst = lds_addr(smem + stage * PAIR + 8 * wv * D);
+    if (half != 1) return;
+    const uint32_t dst = lds_addr(smem + stage * PAIR);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int row0 = doc_start + (2 * p + t) * BN;
@@ -96,8 +100,10 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          dma16_opaque(r[x], dst + ((2 * t + x) * TILE + 4 * j * D) * 2, coff[j]);
+        for (int jj = 0; jj < 4; ++jj)
+          dma16_opaque(r[x],
+                       dst + ((2 * t + x) * TILE + (8 * (ws + 4 * (jj >> 1)) + 4 * (jj & 1)) * D) * 2,
+                       coff[jj]);
     }
   };
 
