@@ -303,7 +303,8 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
                     [&](int r) { return o + (long)(wq0 + r) * qrow + h * D + 64 * H; },
                     doc_end - wq0);
     if (!q_valid) return;
-    if (H == 0 && hi == 0) lse[(long)h * n_tokens + my_q] = (m_tot + fast_log2(l_tot)) * kLn2;
+    if (H == 0 && hi == 0)
+      __builtin_nontemporal_store((m_tot + fast_log2(l_tot)) * kLn2, &lse[(long)h * n_tokens + my_q]);
   };
   if (half) merge(std::integral_constant<int, 1>{});
   else merge(std::integral_constant<int, 0>{});
