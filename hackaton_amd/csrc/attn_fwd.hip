@@ -10,12 +10,13 @@
 // Per wave: Q (staged once through LDS from coalesced row loads) stays in registers as the MFMA B
 // operand; S^T = K Q^T (v_mfma_f32_32x32x16) puts one query per lane, so the online softmax is
 // in-lane plus one v_permlane32_swap; O^T += V^T P^T reads V^T straight from the row-major tile
-// with ds_read_b64_tr_b16. K/V tiles stream through two LDS stages of tile pairs (plain row-major
-// copies, row stride 136 halfs); the next pair's global loads are in flight while the current
-// pair is computed, one barrier per pair. Loads are buffer loads bounded at the document end: rows
-// past it read as zeros (masked keys, zero P). The running maximum moves lazily (only when a tile
-// exceeds it by more than 2^8), so P stays below 256 and the O / l rescale is skipped on most
-// tiles.
+// with ds_read_b64_tr_b16. K/V tiles stream through two LDS stages of tile pairs, copied straight
+// from HBM into LDS by buffer loads that write LDS (256-byte rows, 16-byte chunks XOR-swizzled by
+// swz16 so that the K and V^T reads hit disjoint banks); the next pair's copies are in flight
+// while the current pair is computed, one barrier per pair. Loads are buffer loads bounded at the
+// document end: rows past it read as zeros (masked keys, zero P). The running maximum moves
+// lazily (only when a tile exceeds it by more than 2^8), so P stays below 256 and the O / l
+// rescale is skipped on most tiles. Results leave through non-temporal stores.
 #include <type_traits>
 
 #include "va_common.h"
