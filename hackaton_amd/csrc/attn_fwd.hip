@@ -7,7 +7,7 @@
 // the work item is split in two. At the end the halves swap their unnormalised partial O through
 // LDS and publish (m, l); each half finishes 64 of the 128 columns, half 0 also the log-sum-exp.
 //
-// Per wave: Q (staged once through LDS from coalesced row loads) stays in registers as the MFMA B
+// Per wave: Q (copied once into LDS, read back as each lane's row) stays in registers as the MFMA B
 // operand; S^T = K Q^T (v_mfma_f32_32x32x16) puts one query per lane, so the online softmax is
 // in-lane plus one v_permlane32_swap; O^T += V^T P^T reads V^T straight from the row-major tile
 // with ds_read_b64_tr_b16. K/V tiles stream through two LDS stages of tile pairs, copied straight
@@ -33,7 +33,6 @@ constexpr int BN = 64;          // keys per tile
 constexpr int D = kHeadDim;
 constexpr int TILE = BN * D;    // halfs per K or V tile: 256-byte rows, chunks swizzled by swz16
 constexpr int PAIR = 4 * TILE;  // K0, V0, K1, V1 of one tile pair
-constexpr int LQ = D + 8;       // LDS row stride (halfs) of the Q tile, staged once
 constexpr float kRescaleLog2 = 8.f;     // largest P before the running maximum must move
 static_assert(NT == 512 && BN == 64, "pair copy map: 2 groups of 4 rows per wave and tile");
 static_assert(BM == kFwdBlockM, "the plan's query tile");
@@ -75,7 +74,6 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   // lands in chunk slot i & 15 of row i >> 4 of the group, so it fetches logical chunk
   // (i & 15) ^ swz16(row). Loads are bounded at the document end: rows past it read as zeros
   // (masked keys, zero P).
-  const int srow = tid >> 4, scol = 8 * (tid & 15);  // Q staging: 16 lanes per 256-byte row
   // Only the waves of half 1 copy: a copy instruction stalls its wave on the memory queue until
   // the CU takes it (64 KB per pair enter the CU at ~80 B/clk), and with one copying wave per
   // SIMD the other one starts its MFMAs at once, so the two run out of phase. Wave (1, s) moves
@@ -218,25 +216,30 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   // The two waves of a SIMD come from different halves; the younger one (half 1) would otherwise
   // lose every issue tie and finish each pair last, keeping the others at the barrier.
   if (half) __builtin_amdgcn_s_setprio(1);
-  // Q of the item's 128 queries: coalesced buffer loads (16 lanes per row, rows past the document
-  // end read as zeros), staged through the second LDS stage, which is free until the loop stores
-  // the second tile pair. Each lane then reads its query's row as the B operand of S^T = K Q^T
-  // (column = this lane's query, k slots = d).
-  {
+  // Q of the item's 128 queries, copied straight into the second LDS stage (free until the loop
+  // copies the second tile pair) as swizzled 256-byte rows, by the waves of half 0 while half 1
+  // copies the first tile pair: wave (0, s) moves its strip's rows 32 s .. 32 s + 31, 4 per
+  // instruction. Rows past the document end read as zeros. Each lane then reads its query's row
+  // as the B operand of S^T = K Q^T (column = this lane's query, k slots = d).
+  static_assert(BM * D <= PAIR, "the Q tile fits in one stage");
+  if (half == 0) {
     const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(h + 1) * D) * 2;
-    const brsrc rq = make_rsrc(q + (long)q0 * qrow, bytes);
-    u32x4 xq[BM / 32];
+    const u32x4 rq = make_rsrc4(q + (long)q0 * qrow, bytes);
 #pragma unroll
-    for (int i = 0; i < BM / 32; ++i) xq[i] = bload16(rq, ((srow + 32 * i) * (int)qrow + h * D + scol) * 2);
-    copy_pair(0, 0);
-#pragma unroll
-    for (int i = 0; i < BM / 32; ++i) st128(smem + PAIR + (srow + 32 * i) * LQ + scol, xq[i]);
+    for (int j = 0; j < 8; ++j) {
+      const int r = 32 * strip + 4 * j + (lane >> 4);
+      dma16_opaque(rq, lds_addr(smem + PAIR + (32 * ws + 4 * j) * D),
+                   (r * (int)qrow + h * D + 8 * ((lane & 15) ^ swz16(r))) * 2);
+    }
   }
-  static_assert(BM * LQ <= PAIR, "the Q tile fits in one stage");
+  copy_pair(0, 0);
   wait_vmcnt<0>();
   __syncthreads();
+  {
+    const int r = 32 * strip + l32, f = swz16(r);
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + PAIR + (32 * strip + l32) * LQ + 16 * kk + 8 * hi);
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + PAIR + r * D + 8 * ((2 * kk + hi) ^ f));
+  }
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
   __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
