@@ -10,8 +10,6 @@
 
 namespace va {
 
-constexpr int kWave = 64;
-
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -113,11 +111,6 @@ __device__ inline float max_with_other_half(float x) {
   swap_halves(x, r0, r1);
   return fmaxf(r0, r1);
 }
-// The same through ds_bpermute: no inline asm, so it does not end a scheduling region (code that
-// the compiler should interleave with MFMAs uses this one).
-__device__ inline float max_with_other_half_sched(float x) {
-  return fmaxf(x, __shfl_xor(x, 32));
-}
 __device__ inline float sum_with_other_half(float x) {
   float r0, r1;
   swap_halves(x, r0, r1);
@@ -152,29 +145,6 @@ __device__ __host__ inline int perm32(int r) {  // physical row r = 8g + 4h + i 
   return 16 * (g >> 1) + 8 * h + 4 * (g & 1) + i;
 }
 __device__ __host__ inline int reg_row(int j, int hi) { return 16 * (j >> 3) + 8 * hi + (j & 7); }
-
-// LDS tiles are arrays of 16-byte chunks (8 elements). Row-major tiles of 128 columns hold 16
-// chunks per row; the chunk index is XORed with `swz8(row)` so that the 8 rows one group of 8
-// lanes reads through perm32 ({b..b+3, b+8..b+11}) land in 8 different bank quads, and so that
-// rows written by the coalesced global->LDS copies spread too.
-__device__ inline int swz8(int r) {
-  return ((r & 3) | (((r >> 3) & 1) << 2)) ^ ((r >> 4) & 7);
-}
-// Tiles with 4 chunks per row (32 columns): 2 rows share one bank sweep.
-__device__ inline int swz4(int r) {
-  return (((r >> 1) & 1) | (((r >> 3) & 1) << 1)) ^ ((r >> 4) & 3);
-}
-
-// Element offset of (row, col) in a tile with `CHUNKS` 16-byte chunks per row.
-template <int CHUNKS>
-__device__ inline int tile_off(int row, int col) {
-  static_assert(CHUNKS == 4 || CHUNKS == 8 || CHUNKS == 16, "tile width");
-  const int chunk = col >> 3;
-  int sw;
-  if constexpr (CHUNKS == 4) sw = swz4(row);
-  else sw = swz8(row);
-  return row * (CHUNKS * 8) + (((chunk ^ sw) & (CHUNKS - 1)) << 3) + (col & 7);
-}
 
 // ---------------------------------------------------------------------------------------------
 // LDS access through address-space-3 pointers, so that per-lane bases plus compile-time offsets
@@ -211,29 +181,6 @@ __device__ inline u32x4 pack8_tr(const float* v) {
   return pack8<E>(v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]);
 }
 
-typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
-__device__ inline void st64(lds_u16* p, u32x2 v) { *reinterpret_cast<lds_u32x2*>(p) = v; }
-
-// Register transpose of a 4 x 8 block of 16-bit values: r[i] holds row i (8 columns, two per
-// register), c[j] receives column j as {row0 | row1 << 16, row2 | row3 << 16}. v_perm_b32 picks
-// the low (selector 0x05040100) or high (0x07060302) halves of two registers.
-__device__ inline void transpose4x8(const u32x4 (&r)[4], u32x2 (&c)[8]) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    c[2 * m] = u32x2{__builtin_amdgcn_perm(r[1][m], r[0][m], 0x05040100u),
-                     __builtin_amdgcn_perm(r[3][m], r[2][m], 0x05040100u)};
-    c[2 * m + 1] = u32x2{__builtin_amdgcn_perm(r[1][m], r[0][m], 0x07060302u),
-                         __builtin_amdgcn_perm(r[3][m], r[2][m], 0x07060302u)};
-  }
-}
-
-__device__ inline u32x4 lds_read16(const uint16_t* base, int elem_off) {
-  return *reinterpret_cast<const u32x4*>(base + elem_off);
-}
-__device__ inline void lds_write16(uint16_t* base, int elem_off, u32x4 v) {
-  *reinterpret_cast<u32x4*>(base + elem_off) = v;
-}
-
 __device__ inline u32x4 gload16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Raw buffer resource over [base, base + bytes) (wave-uniform operands, built in SGPRs): a load at
@@ -249,19 +196,14 @@ __device__ inline u32x4 bload16(brsrc r, int byte_off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
 // Buffer load straight into LDS (gfx950 buffer_load_dwordx4 ... lds): lane i's 16 bytes land at
-// dst + 16 i bytes, dst being wave-uniform (it goes through M0). Completion is counted by vmcnt;
-// the compiler does not track the LDS write, so readers wait with wait_vmcnt and a barrier.
-__device__ inline void dma16(brsrc r, lds_u16* dst, int byte_off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
-                                           byte_off, 0, 0, 0);
-}
-// The same copy issued as inline assembly, invisible to the compiler's wait-count tracking: the
-// compiler treats an LDS-writing buffer load as a possible writer of every later transposed LDS
-// read and waits for it to land before each one, which would serialise the copy of the next tile
-// with the MFMAs of the current one. Callers order the copies themselves: wait_vmcnt and a
-// barrier before any wave reads the destination, and the destination not read by any wave since
-// the last barrier. `rsrc` is a buffer descriptor in SGPRs (make_rsrc4), `lds_byte` the
-// wave-uniform LDS byte address of lane 0's 16 bytes.
+// lds_byte + 16 i (M0 holds the wave-uniform base), rows past the buffer's end as zeros;
+// completion is counted by vmcnt. Issued as inline assembly, invisible to the compiler's
+// wait-count tracking: the compiler treats an LDS-writing buffer load as a possible writer of
+// every later transposed LDS read and waits for it to land before each one, which would
+// serialise the copy of the next tile with the MFMAs of the current one. Callers order the copies
+// themselves: wait_vmcnt and a barrier before any wave reads the destination, and the destination
+// not read by any wave since the last barrier. `rsrc` is a buffer descriptor in SGPRs
+// (make_rsrc4), `lds_byte` the LDS byte address of lane 0's 16 bytes.
 __device__ inline void dma16_opaque(u32x4 rsrc, uint32_t lds_byte, int byte_off) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
