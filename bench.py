@@ -8,8 +8,9 @@ resident buffer sets, launched as one captured HIP graph. Inputs are N(0, 1), sy
 Metric: causal-FLOP throughput, F = 3.5 * 4 * Hq * D * sum L(L+1)/2 per call (forward + backward,
 the backward's recomputation of P not counted), in TFLOP/s and as a fraction of the MI355X dense
 fp16 MFMA peak. The dominant kernel's duration is measured with HIP events on the stream it runs
-on (each kernel captured alone, 28 launches per graph replay) and reported against its roofline,
-with the HBM traffic that rocprofv3 --pmc measured for it (profiles/hbm_traffic_<workload>.md). The
+on (each kernel captured alone, 28 launches per graph replay) and reported against its roofline
+(HBM or MFMA, whichever its arithmetic intensity puts first against the ridge point), with the HBM
+traffic that rocprofv3 --pmc measured for it (profiles/hbm_traffic_<workload>.md). The
 CPU baseline is the oracle (numpy fp32) on one layer call of the same shape, on this host's cores.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config 2]
@@ -220,11 +221,23 @@ def main():
     }
     dom_name = max(kernels, key=lambda k: kernels[k]["us"])
     dom = kernels[dom_name]
-    achieved = dom["flops"] / (dom["us"] * 1e-6) / 1e12
-    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": round(achieved, 2),
-                "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+    # The roofline ceiling is set by the kernel's arithmetic intensity (algorithmic FLOPs per
+    # algorithmic HBM byte) against the ridge point peak_mfma / peak_hbm: below it HBM bandwidth
+    # bounds the kernel (achieved = algorithmic bytes / duration), above it the MFMA pipes do.
+    intensity = dom["flops"] / dom["bytes"]
+    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
+    secs = dom["us"] * 1e-6
+    mfma_tflops = dom["flops"] / secs / 1e12
+    if intensity >= ridge:
+        bound, achieved, rpeak, unit = "mfma", mfma_tflops, peak, "TFLOP/s"
+    else:
+        bound, achieved, rpeak, unit = "hbm", dom["bytes"] / secs / 1e9, PEAK_HBM_GBS, "GB/s"
+    roofline = {"kernel": dom_name, "bound": bound, "achieved": round(achieved, 2),
+                "peak": rpeak, "unit": unit, "frac": round(achieved / rpeak, 4),
                 "traffic": measured_traffic(dom_name, cfg["name"]), "avg_us": round(dom["us"], 3),
-                "flops_per_launch": dom["flops"], "algorithmic_bytes": dom["bytes"]}
+                "flops_per_launch": dom["flops"], "algorithmic_bytes": dom["bytes"],
+                "arithmetic_intensity": round(intensity, 1), "ridge": round(ridge, 1),
+                "mfma_tflops": round(mfma_tflops, 2), "mfma_frac": round(mfma_tflops / peak, 4)}
 
     # ---- CPU baseline: the oracle on one layer call of the same shape ------------------------
     cpu = None
