@@ -83,6 +83,24 @@ def measured_traffic(kernel, workload):
     return None
 
 
+def roofline(flops, nbytes, us, peak_tflops, peak_gbs=PEAK_HBM_GBS):
+    """Roofline position of a kernel from its algorithmic FLOPs and HBM bytes per launch and its
+    average launch duration: the ceiling is HBM bandwidth when the arithmetic intensity is below
+    the ridge point peak_tflops / peak_gbs, else the MFMA peak."""
+    intensity = flops / nbytes
+    ridge = peak_tflops * 1e12 / (peak_gbs * 1e9)
+    secs = us * 1e-6
+    mfma_tflops = flops / secs / 1e12
+    if intensity >= ridge:
+        bound, achieved, peak, unit = "mfma", mfma_tflops, peak_tflops, "TFLOP/s"
+    else:
+        bound, achieved, peak, unit = "hbm", nbytes / secs / 1e9, peak_gbs, "GB/s"
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "arithmetic_intensity": round(intensity, 1),
+            "ridge": round(ridge, 1), "mfma_tflops": round(mfma_tflops, 2),
+            "mfma_frac": round(mfma_tflops / peak_tflops, 4)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -221,23 +239,10 @@ def main():
     }
     dom_name = max(kernels, key=lambda k: kernels[k]["us"])
     dom = kernels[dom_name]
-    # The roofline ceiling is set by the kernel's arithmetic intensity (algorithmic FLOPs per
-    # algorithmic HBM byte) against the ridge point peak_mfma / peak_hbm: below it HBM bandwidth
-    # bounds the kernel (achieved = algorithmic bytes / duration), above it the MFMA pipes do.
-    intensity = dom["flops"] / dom["bytes"]
-    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
-    secs = dom["us"] * 1e-6
-    mfma_tflops = dom["flops"] / secs / 1e12
-    if intensity >= ridge:
-        bound, achieved, rpeak, unit = "mfma", mfma_tflops, peak, "TFLOP/s"
-    else:
-        bound, achieved, rpeak, unit = "hbm", dom["bytes"] / secs / 1e9, PEAK_HBM_GBS, "GB/s"
-    roofline = {"kernel": dom_name, "bound": bound, "achieved": round(achieved, 2),
-                "peak": rpeak, "unit": unit, "frac": round(achieved / rpeak, 4),
-                "traffic": measured_traffic(dom_name, cfg["name"]), "avg_us": round(dom["us"], 3),
-                "flops_per_launch": dom["flops"], "algorithmic_bytes": dom["bytes"],
-                "arithmetic_intensity": round(intensity, 1), "ridge": round(ridge, 1),
-                "mfma_tflops": round(mfma_tflops, 2), "mfma_frac": round(mfma_tflops / peak, 4)}
+    roofline_ = {"kernel": dom_name,
+                 **roofline(dom["flops"], dom["bytes"], dom["us"], peak),
+                 "traffic": measured_traffic(dom_name, cfg["name"]), "avg_us": round(dom["us"], 3),
+                 "flops_per_launch": dom["flops"], "algorithmic_bytes": dom["bytes"]}
 
     # ---- CPU baseline: the oracle on one layer call of the same shape ------------------------
     cpu = None
@@ -287,7 +292,7 @@ def main():
         "kernels_us": {k: round(v["us"], 3) for k, v in kernels.items()},
         "kernels_tflops": {k: round(v["flops"] / (v["us"] * 1e-6) / 1e12, 2)
                            for k, v in kernels.items() if v["flops"]},
-        "roofline": roofline,
+        "roofline": roofline_,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
