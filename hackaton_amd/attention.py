@@ -246,7 +246,7 @@ class VarlenAttention(torch.autograd.Function):
         out, lse = attention_forward(query, key, value, plan, scale)
         ctx.save_for_backward(query, key, value, out, lse, cu_seqlens)
         ctx.max_len, ctx.scale, ctx.plan = max_len, scale, plan
-        return out.reshape(query.shape[0], -1)
+        return out.reshape(query.shape[0], query.shape[1] * query.shape[2])
 
     @staticmethod
     def backward(ctx, grad):
@@ -262,6 +262,8 @@ def _lengths_cu(lengths, device):
     if isinstance(lengths, torch.Tensor) and lengths.is_cuda:
         return _device_cu_seqlens(lengths), None
     lengths = [int(length) for length in lengths if int(length) > 0]
+    if not lengths:  # the reference's max() of no lengths raises ValueError too (attention.py:242)
+        raise ValueError("varlen attention: every length is zero (no tokens to attend over)")
     return _cu_seqlens(lengths, device), max(lengths)
 
 
@@ -430,7 +432,7 @@ class PackedAttention(torch.autograd.Function):
             ctx.save_for_backward(*rot, out, lse)
         else:
             ctx.save_for_backward(q, k, v)
-        return out.reshape(q.shape[0], -1).to(_compute_dtype(q.dtype))
+        return out.reshape(out.shape[0], out.shape[1] * out.shape[2]).to(_compute_dtype(q.dtype))
 
     @staticmethod
     def backward(ctx, dout):
