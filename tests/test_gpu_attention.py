@@ -178,8 +178,9 @@ def test_7b_config_longest_documents_match_oracle():
 
 
 def test_forward_and_backward_are_bitwise_deterministic():
-    """No atomics anywhere: dQ and the per-head dK/dV partials are each written by one work-group
-    and the GQA sum adds the partials in head order, so repeated calls agree bit for bit."""
+    """The attention kernels use no atomics: dQ and the per-head dK/dV partials are each written
+    by one work-group and the GQA sum adds the partials in head order, so repeated calls agree
+    bit for bit."""
     lengths, hq, hkv = [512, 300, 77], 12, 2
     banner("determinism", lengths)
     q, k, v, do = wl.make_inputs(lengths, hq, hkv, torch.float16, seed=5)
