@@ -40,6 +40,9 @@ int check_heads(int32_t hq, int32_t hkv) {
   return VA_OK;
 }
 
+constexpr int64_t kKvItemCost = va::kPlanKvItemCost;
+constexpr int64_t kQItemCost = va::kPlanQItemCost;
+
 std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
   std::vector<Item> items;
   for (int32_t i = 0; i < n_docs; ++i) {
@@ -52,17 +55,22 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
         for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, h, work});
       }
     } else {
-      // kv items: the two halves take alternate 32-query steps over the 128 keys
+      // Work of a backward item: MFMAs per wave per step pair (kv items: 32 for each pair of
+      // 32-query steps; q items: 24 for each pair of 32-key tiles) plus the item's fixed cost
+      // (prologue and epilogue) in the same unit. Item durations measured in the benchmark's
+      // graph at 4 x 512 tokens: ~2.4 us per kv step pair + ~3.0 us per kv item, ~1.9 us per q
+      // tile pair + ~2.4 us per q item; hence 39 and 30. Without the fixed cost a kv item over
+      // 384 queries (18.7 us) ties with a q item over 512 keys (17.3 us), and the XCD layout
+      // below deals the heavier ones to the same XCDs in every block.
       for (int32_t k0 = s; k0 < e; k0 += va::kBwdBlockN) {
         const int64_t steps = ((int64_t)e - k0 + va::kBwdBlockQ - 1) / va::kBwdBlockQ;
-        const int64_t work = (steps + 1) / 2 * 32;  // MFMAs per wave per step pair
+        const int64_t work = (steps + 1) / 2 * 32 + kKvItemCost;
         for (int32_t h = 0; h < hq; ++h) items.push_back({k0, e, s, h, work});
       }
-      // q items: the two halves take alternate 32-key tiles up to the diagonal
       for (int32_t q0 = s; q0 < e; q0 += va::kBwdBlockM) {
         const int64_t kv_end = std::min<int64_t>((int64_t)q0 + va::kBwdBlockM, e);
         const int64_t tiles = (kv_end - s + va::kBwdTileK - 1) / va::kBwdTileK;
-        const int64_t work = (tiles + 1) / 2 * 24;
+        const int64_t work = (tiles + 1) / 2 * 24 + kQItemCost;
         for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, (1 << 24) | h, work});
       }
     }

@@ -123,11 +123,11 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       work = min(s + (long)(t + 1) * kTile, e) - s;
     } else if (!is_q) {
       const long steps = (e - (s + (long)t * kTile) + kBwdBlockQ - 1) / kBwdBlockQ;
-      work = (steps + 1) / 2 * 32;
+      work = (steps + 1) / 2 * 32 + kPlanKvItemCost;
     } else {
       const long kv_end = min(s + (long)(t + 1) * kTile, e);
       const long tiles = (kv_end - s + kBwdTileK - 1) / kBwdTileK;
-      work = (tiles + 1) / 2 * 24;
+      work = (tiles + 1) / 2 * 24 + kPlanQItemCost;
     }
     const long b = work >> 3;
     return (int)(b >= kBuckets ? kBuckets - 1 : b);

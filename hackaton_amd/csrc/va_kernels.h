@@ -16,6 +16,10 @@ constexpr int kBwdBlockQ = 32;   // queries per kv-item step
 constexpr int kBwdBlockM = 128;  // queries per backward q work item
 constexpr int kBwdTileK = 32;    // keys per q-item tile
 constexpr int kPlanMaxDocs = 8192;  // documents a device-built plan takes (LDS-resident bounds)
+// Fixed cost of a backward kv / q item (prologue, epilogue) in the planners' work unit, MFMAs per
+// wave per step pair: 32 per kv step pair, 24 per q tile pair (from in-graph item durations).
+constexpr int kPlanKvItemCost = 39;
+constexpr int kPlanQItemCost = 30;
 
 struct FwdArgs {
   const void* q;

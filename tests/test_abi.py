@@ -75,6 +75,21 @@ def check_xcd_order(items, hq, hkv, work_of):
     assert work == sorted(work, reverse=True)
 
 
+def test_backward_plan_deals_every_xcd_the_same_items():
+    """Four 512-token documents: work-group i runs on XCD i mod 8, and every XCD gets the same
+    mix of item kinds and spans. (With no per-item cost in the work measure, kv items over 384
+    queries tie with q items over 512 keys, and the block layout sent all of the former to half
+    of the XCDs.)"""
+    hq, hkv = 12, 2
+    _, items = plan([512] * 4, hq, hkv, _lib.VA_PLAN_BWD)
+    mixes = []
+    for x in range(8):
+        mix = sorted((w >> 24, (e - a) if w >> 24 == 0 else min(a + 128, e) - s)
+                     for a, e, s, w in items[x::8].tolist())
+        mixes.append(mix)
+    assert all(m == mixes[0] for m in mixes)
+
+
 @pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1], [257, 3]])
 def test_backward_plan_covers_every_key_and_query_tile_once(lengths):
     """kv items (dK/dV of 128 keys) and q items (dQ of 128 queries), one per head each."""
@@ -93,10 +108,10 @@ def test_backward_plan_covers_every_key_and_query_tile_once(lengths):
     assert kv_seen == expected and q_seen == expected
     assert len(items) == 2 * len(expected)
 
-    def work(a, e, s, w):  # the planner's measure: MFMAs per wave per step pair
+    def work(a, e, s, w):  # the planner's measure: MFMAs per wave per step pair + item cost
         if w >> 24 == 0:
-            return ((e - a + 31) // 32 + 1) // 2 * 32
-        return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24
+            return ((e - a + 31) // 32 + 1) // 2 * 32 + 39
+        return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
     check_xcd_order(items, hq, hkv, work)
 
 
