@@ -386,10 +386,15 @@ def test_device_plan_matches_host_plan(lengths):
         real, empty = got[: len(host)], got[len(host):]
         assert sorted(map(tuple, real.tolist())) == sorted(map(tuple, host.tolist()))
         assert not empty.any()
-        # longest first by the planner's work measure (buckets of 8 apart)
+        # longest first by the planner's work measure (buckets of 8 apart): keys visited
+        # (forward); MFMAs per wave per step pair plus the item's fixed cost (backward)
         if kind == 0:
             work = [min(q0 + 128, e) - s for q0, e, s, _ in real.tolist()]
-            assert all(a // 8 >= b // 8 for a, b in zip(work, work[1:]))
+        else:
+            work = [((e - a + 31) // 32 + 1) // 2 * 32 + 39 if w >> 24 == 0
+                    else ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
+                    for a, e, s, w in real.tolist()]
+        assert all(x // 8 >= y // 8 for x, y in zip(work, work[1:]))
 
 
 def test_device_lengths_run_without_host_reads_and_match_host_lengths():
