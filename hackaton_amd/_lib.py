@@ -13,7 +13,7 @@ VA_OK, VA_EINVAL, VA_ESHAPE, VA_EDTYPE, VA_ESEQ, VA_ECAPACITY = 0, -1, -2, -3, -
 VA_F16, VA_BF16, VA_F32 = 0, 1, 2
 VA_PLAN_FWD, VA_PLAN_BWD = 0, 1
 VA_LAYOUT_PACKED, VA_LAYOUT_PADDED = 0, 1
-VA_BWD_PREPARE, VA_BWD_MAIN, VA_BWD_FINISH = 0, 1, 2
+VA_BWD_MAIN, VA_BWD_FINISH = 1, 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -31,6 +31,9 @@ SIGNATURES = {
     "va_plan_build": (ctypes.c_int, [_pi32, _i32, _i32, _i32, _i32, _pi32, _i64, _pi64]),
     "va_plan_capacity": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64]),
     "va_plan_build_device": (ctypes.c_int, [_p, _i32, _i64, _i32, _i32, _i32, _p, _i64, _p]),
+    "va_plan_build_device_lengths": (ctypes.c_int, [_p, _i32, _i64, _i32, _i32, _p, _i64, _p,
+                                                    _i64, _p, _p]),
+    "va_stream_capture_id": (ctypes.c_int, [_p, ctypes.POINTER(ctypes.c_uint64)]),
     "va_fwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _i32,
                               _p]),
     "va_bwd_workspace_layout": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64, _pi64]),

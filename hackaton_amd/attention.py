@@ -23,6 +23,8 @@ Differences that keep the drop-in contract:
 Every op requires the HIP library and CUDA (HIP) tensors; there is no other implementation.
 """
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -68,9 +70,9 @@ _PLANS = {}
 
 
 def _cu_seqlens(lengths, device):
-    """int32 [0, l0, l0 + l1, ...] on the device, built once per batch shape (the 28 layers share
-    it), as solution/attention.py:198-209. The lengths ride along on the tensor so the work plan
-    is built on the host without reading the device."""
+    """Document start offsets (and the total) as an int32 device tensor, one tensor per distinct
+    list of lengths and device, reused by every layer of a step (solution/attention.py:198-209).
+    The host copy of the offsets is attached to the tensor, so the planner never reads the GPU."""
     key = (device, tuple(lengths))
     cu = _CU_SEQLENS.get(key)
     if cu is None:
@@ -119,42 +121,67 @@ def build_plan_host(cu, hq, hkv, kind):
 
 
 class DevicePlan:
-    """Work lists built on the device from a device cu_seqlens (va_plan_build_device): no host
-    read of the lengths. Each list has the capacity that the host-known sizes bound; its slots past
-    the real items are empty items that the kernels skip."""
+    """Work lists and cu_seqlens built on the device from device lengths by one launch
+    (va_plan_build_device_lengths): no host read. Each list has the capacity that the host-known
+    sizes bound; its slots past the real items are empty items that the kernels skip."""
 
-    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total")
+    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "cu", "__weakref__")
 
-    def __init__(self, cu_seqlens, n_tokens, hq, hkv):
-        n_docs = cu_seqlens.shape[0] - 1
+    def __init__(self, lengths, n_tokens, hq, hkv):
+        lengths = lengths.reshape(-1)
+        if lengths.dtype != torch.int64:
+            lengths = lengths.to(torch.int64)
+        lengths = lengths.contiguous()
+        n_docs = lengths.numel()
         self.total = int(n_tokens)
-        stream = _stream()
-        lists = []
+        dev = lengths.device
+        caps = []
         for kind in (_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD):
             cap = np.zeros(1, dtype=np.int64)
             check(lib().va_plan_capacity(n_tokens, n_docs, hq, kind, cap.ctypes.data_as(_lib._pi64)),
                   "va_plan_capacity")
-            items = torch.empty(max(int(cap[0]), 1), 4, dtype=torch.int32,
-                                device=cu_seqlens.device)
-            check(lib().va_plan_build_device(cu_seqlens.data_ptr(), n_docs, n_tokens, hq, hkv, kind,
-                                             items.data_ptr(), int(cap[0]), stream),
-                  "va_plan_build_device")
-            lists.append((items, int(cap[0])))
-        (self.fwd_items, self.n_fwd), (self.bwd_items, self.n_bwd) = lists
+            caps.append(int(cap[0]))
+        self.n_fwd, self.n_bwd = caps
+        self.fwd_items = torch.empty(max(self.n_fwd, 1), 4, dtype=torch.int32, device=dev)
+        self.bwd_items = torch.empty(max(self.n_bwd, 1), 4, dtype=torch.int32, device=dev)
+        self.cu = torch.empty(n_docs + 1, dtype=torch.int32, device=dev)
+        check(lib().va_plan_build_device_lengths(
+            lengths.data_ptr() if n_docs else None, n_docs, n_tokens, hq, hkv,
+            self.fwd_items.data_ptr(), self.n_fwd, self.bwd_items.data_ptr(), self.n_bwd,
+            self.cu.data_ptr(), _stream()), "va_plan_build_device_lengths")
+        self.cu._va_plan = self
 
 
-def _device_cu_seqlens(lengths):
-    """int32 [0, l0, l0 + l1, ...] on the device from a device tensor of lengths, with no host
-    read (zero lengths are empty documents: they produce no work)."""
-    cu = torch.zeros(lengths.numel() + 1, dtype=torch.int32, device=lengths.device)
-    cu[1:] = torch.cumsum(lengths.reshape(-1).to(torch.int64).clamp(min=0), 0).to(torch.int32)
-    return cu
+def _capture_id():
+    cid = ctypes.c_uint64(0)
+    check(lib().va_stream_capture_id(_stream(), ctypes.byref(cid)), "va_stream_capture_id")
+    return cid.value
 
 
-def _plan(cu_seqlens, hq, hkv, n_tokens=None):
+def _device_plan(lengths, n_tokens, hq, hkv):
+    """The device plan of a device lengths tensor, built once and reused by every layer that gets
+    the same tensor (unchanged since: its version counter is part of the key). A plan built while
+    a graph is being captured is reused only inside that same capture, and one built outside any
+    capture never inside one: a captured graph then always contains the plan build its replays
+    need."""
+    key = (lengths._version, int(n_tokens), hq, hkv, _capture_id())
+    cache = getattr(lengths, "_va_plans", None)
+    if cache is None:
+        cache = {}
+        lengths._va_plans = cache
+    plan = cache.get(key)
+    if plan is None:
+        if len(cache) > 8:
+            cache.clear()
+        plan = cache[key] = DevicePlan(lengths, n_tokens, hq, hkv)
+    return plan
+
+
+def _plan(cu_seqlens, hq, hkv):
+    device_plan = getattr(cu_seqlens, "_va_plan", None)
+    if device_plan is not None:
+        return device_plan
     offsets = getattr(cu_seqlens, "_va_offsets", None)
-    if offsets is None and n_tokens is not None and cu_seqlens.is_cuda:
-        return DevicePlan(cu_seqlens, n_tokens, hq, hkv)
     if offsets is None:  # a cu_seqlens tensor not made by _cu_seqlens: read it (one sync)
         offsets = tuple(int(x) for x in cu_seqlens.cpu().tolist())
     key = (cu_seqlens.device, offsets, hq, hkv)
@@ -235,14 +262,14 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
 
 
 class VarlenAttention(torch.autograd.Function):
-    """Causal attention of every document of the packed rows in one launch of the gfx950 forward
-    kernel (and three of the backward), given the document boundaries `cu_seqlens`.
-    Inputs (N, H, D) query and (N, Hkv, D) key/value (Hkv = H, the reference's expanded form, or
-    the GQA kv heads), output (N, H * D). solution/attention.py:212-233."""
+    """Autograd node of the attention itself: one forward launch over all documents of the packed
+    rows, and the backward launches, driven by a work plan built from `cu_seqlens`. Query rows
+    (N, H, D); key/value rows (N, Hkv, D) with Hkv dividing H (Hkv = H is the expanded form the
+    reference passes). Returns (N, H * D). Replaces solution/attention.py:212-233."""
 
     @staticmethod
     def forward(ctx, query, key, value, cu_seqlens, max_len, scale):
-        plan = _plan(cu_seqlens, query.shape[1], key.shape[1], query.shape[0])
+        plan = _plan(cu_seqlens, query.shape[1], key.shape[1])
         out, lse = attention_forward(query, key, value, plan, scale)
         ctx.save_for_backward(query, key, value, out, lse, cu_seqlens)
         ctx.max_len, ctx.scale, ctx.plan = max_len, scale, plan
@@ -255,12 +282,12 @@ class VarlenAttention(torch.autograd.Function):
         return dq, dk, dv, None, None, None
 
 
-def _lengths_cu(lengths, device):
+def _lengths_cu(lengths, device, hq, hkv, n_tokens):
     """cu_seqlens for `lengths`: a host list (zero lengths dropped, as solution/attention.py:239;
-    the plan is built on the host and cached) or a device tensor (cu_seqlens and the plan are
-    built on the device: no host read, no synchronisation)."""
+    the plan is built on the host and cached) or a device tensor (cu_seqlens and both plans are
+    built on the device by one launch, cached on the tensor: no host read, no synchronisation)."""
     if isinstance(lengths, torch.Tensor) and lengths.is_cuda:
-        return _device_cu_seqlens(lengths), None
+        return _device_plan(lengths, n_tokens, hq, hkv).cu, None
     lengths = [int(length) for length in lengths if int(length) > 0]
     if not lengths:  # the reference's max() of no lengths raises ValueError too (attention.py:242)
         raise ValueError("varlen attention: every length is zero (no tokens to attend over)")
@@ -268,10 +295,13 @@ def _lengths_cu(lengths, device):
 
 
 def varlen_attention(query, key, value, lengths, scale):
-    """Causal attention of each sequence on its own, on packed (N, H, D) rows where sequence i is
-    the contiguous block of `lengths[i]` rows; returns (N, H * D). solution/attention.py:236-242.
-    `lengths` may also be a device tensor: then nothing is read back to the host."""
-    cu_seqlens, max_len = _lengths_cu(lengths, query.device)
+    """Packed rows hold documents back to back, document i being the next `lengths[i]` rows; each
+    query row attends causally to the rows of its own document only. Returns (N, H * D).
+    `lengths` is a host list (zero entries are skipped) or a device tensor, in which case the
+    document offsets and the work plan are built on the GPU with no host read.
+    Same call as solution/attention.py:236-242."""
+    cu_seqlens, max_len = _lengths_cu(lengths, query.device, query.shape[1], key.shape[1],
+                                      query.shape[0])
     return VarlenAttention.apply(query.contiguous(), key.contiguous(), value.contiguous(),
                                  cu_seqlens, max_len, scale)
 
@@ -339,9 +369,11 @@ def rope_backward(dq, dk, dv, cos, sin, b_idx, t_idx, heads, kv_heads, out_dtype
 
 
 class QKVRotate(torch.autograd.Function):
-    """Packed (q, k, v) projections (N, heads * D) -> rotated, fp16, GQA-expanded heads:
-    (N, H, D) each when `padded` is False, (B, H, T, D) each when it is True.
-    solution/attention.py:150-188 (same outputs and the same 12 returned gradients)."""
+    """Rotary embedding of the query and key projections plus the fp16 cast of the values, with
+    key/value heads repeated to the query-head count. Projections come in as packed rows
+    (N, heads * D); the three results are packed (N, heads, D) rows, or a zero-filled
+    (B, heads, T, D) batch when `padded` is set. Backward: the inverse rotation, after summing the
+    repeated heads. Same outputs and 12 returned gradients as solution/attention.py:150-188."""
 
     @staticmethod
     def forward(ctx, q, k, v, cos, sin, b_idx, t_idx, batch, seq, heads, kv_heads, padded):
@@ -377,8 +409,8 @@ def _compute_dtype(proj_dtype):
 def _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lengths, scale):
     """Rotation (no K/V expansion) + varlen attention; returns (out (N,Hq,D), lse, rotated q/k/v,
     plan). solution/attention.py:245-247."""
-    cu, _max_len = _lengths_cu(lengths, q.device)
-    plan = _plan(cu, heads, kv_heads, q.shape[0])
+    cu, _max_len = _lengths_cu(lengths, q.device, heads, kv_heads, q.shape[0])
+    plan = _plan(cu, heads, kv_heads)
     qr, kr, vr = rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads,
                               _compute_dtype(q.dtype))
     out, lse = attention_forward(qr, kr, vr, plan, scale)
@@ -405,7 +437,8 @@ def set_save_policy(policy):
 
 
 class PackedAttention(torch.autograd.Function):
-    """Rotation + per-sequence causal attention of the packed rows, (N, heads * D) out.
+    """Autograd node of the decoder layer's call: rotary embedding, then causal attention of every
+    document of the packed rows; returns (N, heads * D) in the compute type.
 
     The backward runs the attention backward kernels (dK/dV summed over each GQA group in fp32)
     and the inverse rotation straight from the fp32 accumulators. What is kept for it follows
@@ -466,8 +499,9 @@ def packed_attention(q, k, v, cos, sin, b_idx, t_idx, seq, heads, kv_heads, leng
 # padded -> packed rows (fallback layout)
 # ------------------------------------------------------------------------------------------------
 class PackRows(torch.autograd.Function):
-    """(B, H, T, D) attention output -> (N, H * D) rows of the real tokens (fallback path).
-    solution/attention.py:303-325."""
+    """Gathers the real tokens of a padded (B, H, T, D) attention result into packed
+    (N, H * D) rows for the output projection; the backward scatters the row gradients back into
+    a zero-filled padded tensor. Used by the masked fallback. solution/attention.py:303-325."""
 
     @staticmethod
     def forward(ctx, attn, b_idx, t_idx):

@@ -145,7 +145,7 @@ extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, cons
                             int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype,
                             void* dq, void* dk, void* dv, void* workspace,
                             int64_t workspace_bytes, void* stream) {
-  if (stage < VA_BWD_PREPARE || stage > VA_BWD_FINISH)
+  if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH)
     return va::fail(VA_EINVAL, "va_bwd_stage: stage %d", stage);
   return bwd_common(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
                     head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
@@ -176,6 +176,11 @@ int rope_common(const void* x0, const void* x1, const void* x2, const float* cos
                         (const void*)t_idx, (const void*)y0, (const void*)y1, (const void*)y2}) {
     if (p == nullptr) return va::fail(VA_EINVAL, "%s: NULL buffer", what);
   }
+  // 16-byte lane accesses: tensor bases and the cos/sin row starts must be 16-byte aligned.
+  for (const void* p : {x0, x1, x2, (const void*)cos, (const void*)sin, (const void*)y0,
+                        (const void*)y1, (const void*)y2}) {
+    if (!aligned16(p)) return va::fail(VA_EINVAL, "%s: buffer not 16-byte aligned", what);
+  }
   return VA_OK;
 }
 
@@ -191,6 +196,9 @@ extern "C" int va_rope_fwd(const void* q, const void* k, const void* v, const fl
                        kv_heads, head_dim, seq, in_dtype, out_dtype, layout, expand,
                        "va_rope_fwd");
   if (rc || n_tokens == 0) return rc;
+  if (cos_batch_stride % 4 != 0 || cos_seq_stride % 4 != 0 || cos_batch_stride < 0 ||
+      cos_seq_stride < 0)
+    return va::fail(VA_EINVAL, "va_rope_fwd: cos/sin strides must be non-negative multiples of 4");
   va::RopeArgs a{q, k, v, cos, sin, cos_batch_stride, cos_seq_stride, b_idx, t_idx,
                  q_out, k_out, v_out, n_tokens, heads, kv_heads, seq, in_dtype, out_dtype,
                  layout, expand, (hipStream_t)stream};
@@ -208,6 +216,9 @@ extern "C" int va_rope_bwd(const void* dq, const void* dk, const void* dv, const
                        kv_heads, head_dim, seq, in_dtype, out_dtype, layout, expand,
                        "va_rope_bwd");
   if (rc || n_tokens == 0) return rc;
+  if (cos_batch_stride % 4 != 0 || cos_seq_stride % 4 != 0 || cos_batch_stride < 0 ||
+      cos_seq_stride < 0)
+    return va::fail(VA_EINVAL, "va_rope_bwd: cos/sin strides must be non-negative multiples of 4");
   va::RopeArgs a{dq, dk, dv, cos, sin, cos_batch_stride, cos_seq_stride, b_idx, t_idx,
                  dq_in, dk_in, dv_in, n_tokens, heads, kv_heads, seq, in_dtype, out_dtype,
                  layout, expand, (hipStream_t)stream};

@@ -502,8 +502,13 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
   lds_u16* smem = (lds_u16*)smem_raw;
   const int4 it = items[blockIdx.x];
-  if (it.x >= it.y) return;  // an empty slot of a device-built plan
-  if ((it.w >> 24) == bwd::kKindKV) {
+  // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
+  // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
+  const int kind = it.w >> 24, h = it.w & 0xffffff;
+  if (it.x >= it.y || it.z < 0 || it.x < it.z || it.y > n_tokens || h >= hq ||
+      (kind != bwd::kKindKV && kind != bwd::kKindQ))
+    return;
+  if (kind == bwd::kKindKV) {
     bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,
                    scale, scale_log2);
   } else {
@@ -579,11 +584,8 @@ static hipError_t launch_bwd_finish_t(const BwdArgs& a) {
 
 hipError_t launch_bwd_stage(const BwdArgs& a, int stage) {
   const bool bf = a.dtype != 0;
-  switch (stage) {
-    case 0: return hipSuccess;  // nothing to prepare: delta is computed inside the main kernel
-    case 1: return bf ? launch_bwd_main_t<BF16>(a) : launch_bwd_main_t<F16>(a);
-    default: return bf ? launch_bwd_finish_t<BF16>(a) : launch_bwd_finish_t<F16>(a);
-  }
+  if (stage == 1) return bf ? launch_bwd_main_t<BF16>(a) : launch_bwd_main_t<F16>(a);
+  return bf ? launch_bwd_finish_t<BF16>(a) : launch_bwd_finish_t<F16>(a);
 }
 
 hipError_t launch_bwd(const BwdArgs& a) {

@@ -51,7 +51,10 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
 
   const int4 it = items[blockIdx.x];
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w;
-  if (q0 >= doc_end) return;  // an empty slot of a device-built plan
+  // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
+  // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
+  if (q0 >= doc_end || doc_start < 0 || q0 < doc_start || doc_end > n_tokens || h < 0 || h >= hq)
+    return;
   const int group = hq / hkv;
   const int kvh = h / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;

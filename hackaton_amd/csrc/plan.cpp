@@ -173,22 +173,72 @@ extern "C" int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, in
   return VA_OK;
 }
 
-extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs,
-                                    int64_t n_tokens, int32_t hq, int32_t hkv, int32_t kind,
-                                    int32_t* items_device, int64_t capacity, void* stream) {
+namespace {
+
+int check_device_plan(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
+                      const int32_t* items, int64_t capacity) {
   int64_t need = 0;
   int rc = va_plan_capacity(n_tokens, n_docs, hq, kind, &need);
   if (rc) return rc;
-  rc = check_heads(hq, hkv);
-  if (rc) return rc;
-  if (cu_seqlens_device == nullptr || items_device == nullptr)
-    return va::fail(VA_EINVAL, "cu_seqlens_device / items_device is NULL");
-  if (((uintptr_t)items_device & 15u) != 0) return va::fail(VA_EINVAL, "items_device not 16-byte aligned");
+  if (items == nullptr) return va::fail(VA_EINVAL, "device plan items are NULL");
+  if (((uintptr_t)items & 15u) != 0) return va::fail(VA_EINVAL, "items_device not 16-byte aligned");
   if (capacity < need)
     return va::fail(VA_ECAPACITY, "device plan needs capacity %lld, got %lld", (long long)need,
                     (long long)capacity);
-  const hipError_t e = va::launch_plan_device(cu_seqlens_device, n_docs, (int)n_tokens, hq, kind,
-                                              items_device, (long)capacity, (hipStream_t)stream);
+  return VA_OK;
+}
+
+}  // namespace
+
+extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs,
+                                    int64_t n_tokens, int32_t hq, int32_t hkv, int32_t kind,
+                                    int32_t* items_device, int64_t capacity, void* stream) {
+  int rc = check_heads(hq, hkv);
+  if (rc) return rc;
+  if (kind != VA_PLAN_FWD && kind != VA_PLAN_BWD) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
+  if (cu_seqlens_device == nullptr) return va::fail(VA_EINVAL, "cu_seqlens_device is NULL");
+  if ((rc = check_device_plan(n_tokens, n_docs, hq, hkv, kind, items_device, capacity))) return rc;
+  const bool fwd = kind == VA_PLAN_FWD;
+  const hipError_t e = va::launch_plan_device(
+      cu_seqlens_device, nullptr, n_docs, (int)n_tokens, hq, hkv, fwd ? items_device : nullptr,
+      capacity, fwd ? nullptr : items_device, capacity, nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return va::fail((int)e, "va_plan_build_device launch: %s", hipGetErrorString(e));
+  return VA_OK;
+}
+
+extern "C" int va_plan_build_device_lengths(const int64_t* lengths_device, int32_t n_docs,
+                                            int64_t n_tokens, int32_t hq, int32_t hkv,
+                                            int32_t* fwd_items_device, int64_t fwd_capacity,
+                                            int32_t* bwd_items_device, int64_t bwd_capacity,
+                                            int32_t* cu_seqlens_out, void* stream) {
+  int rc = check_heads(hq, hkv);
+  if (rc) return rc;
+  if (lengths_device == nullptr && n_docs > 0) return va::fail(VA_EINVAL, "lengths_device is NULL");
+  if (fwd_items_device == nullptr && bwd_items_device == nullptr)
+    return va::fail(VA_EINVAL, "no plan requested");
+  if (fwd_items_device != nullptr &&
+      (rc = check_device_plan(n_tokens, n_docs, hq, hkv, VA_PLAN_FWD, fwd_items_device,
+                              fwd_capacity)))
+    return rc;
+  if (bwd_items_device != nullptr &&
+      (rc = check_device_plan(n_tokens, n_docs, hq, hkv, VA_PLAN_BWD, bwd_items_device,
+                              bwd_capacity)))
+    return rc;
+  const hipError_t e = va::launch_plan_device(nullptr, lengths_device, n_docs, (int)n_tokens, hq,
+                                              hkv, fwd_items_device, fwd_capacity,
+                                              bwd_items_device, bwd_capacity, cu_seqlens_out,
+                                              (hipStream_t)stream);
+  if (e != hipSuccess)
+    return va::fail((int)e, "va_plan_build_device_lengths launch: %s", hipGetErrorString(e));
+  return VA_OK;
+}
+
+extern "C" int va_stream_capture_id(void* stream, uint64_t* capture_id) {
+  if (capture_id == nullptr) return va::fail(VA_EINVAL, "capture_id is NULL");
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  const hipError_t e = hipStreamGetCaptureInfo((hipStream_t)stream, &status, &id);
+  if (e != hipSuccess) return va::fail((int)e, "hipStreamGetCaptureInfo: %s", hipGetErrorString(e));
+  *capture_id = status == hipStreamCaptureStatusActive ? (uint64_t)id : 0;
   return VA_OK;
 }

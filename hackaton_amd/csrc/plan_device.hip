@@ -1,14 +1,18 @@
-// Work plans built on the device from a device cu_seqlens, for callers whose document lengths are
-// only on the GPU: no host read, so no stream synchronisation (the reference reads them back with
-// lengths.tolist() at solution/packed.py:170-172).
+// Work plans built on the device, for callers whose document lengths are only on the GPU: no host
+// read, so no stream synchronisation (the reference reads them back with lengths.tolist() at
+// solution/packed.py:170-172).
 //
-// One work-group of 1024 threads: per-document tile counts and their prefix sum in LDS, then a
-// counting sort of the tile candidates by work (the host planner's work measure, in buckets of 8)
-// longest first, then one work item per (candidate, query head). Items inside a bucket come in
-// atomic order: every item is computed on its own, so the order changes no result. The plan is
+// One launch, one 1024-thread work-group per plan kind (forward, backward). Each work-group takes
+// the document bounds (from a device cu_seqlens, or from device lengths through a saturating
+// prefix sum), clamps them into [0, n_tokens] and makes them non-decreasing; counts each
+// document's tiles and prefix-sums the counts in LDS; sorts the tile candidates by the host
+// planner's work measure (counting sort, buckets of 8), longest first; and writes one item per
+// (candidate, query head) in the host planner's XCD layout: every candidate is Hkv combos (one
+// per GQA group), combos are dealt 8 at a time as the columns of a G x 8 block, so that the G
+// heads of a group run on one XCD and share its L2. Candidates inside a bucket come in atomic
+// order: every item is computed on its own, so the order changes no result. Each plan is
 // `capacity` items long; slots past the real items hold empty items that the attention kernels
-// skip at once. Document bounds are clamped into [0, n_tokens] and made non-decreasing, so that
-// any cu_seqlens content yields in-bounds items.
+// skip at once.
 #include <climits>
 
 #include "../../include/varlen_attn.h"
@@ -19,56 +23,96 @@ namespace va {
 
 namespace {
 
-constexpr int PT = 1024;           // threads of the planning work-group
+constexpr int PT = 1024;           // threads of a planning work-group
 constexpr int kBuckets = 4096;     // work buckets of 8
 constexpr int kTile = kFwdBlockM;  // rows of a forward query tile, a kv key tile, a q query tile
+constexpr int kXcds = 8;           // work-group i runs on XCD i mod 8
 static_assert(kBwdBlockN == kTile && kBwdBlockM == kTile, "one tile size for every item kind");
 constexpr int DPB = (kPlanMaxDocs + 1 + PT - 1) / PT;  // document bounds per thread
 constexpr int BPT = kBuckets / PT;                      // buckets per thread
 
 __device__ inline int tiles_of(int len) { return len <= 0 ? 0 : (len + kTile - 1) / kTile; }
 
-// Inclusive block scan of one value per thread (Hillis-Steele over LDS): sum, or max.
-template <bool kMax>
-__device__ int block_scan(int x, int* buf) {
+// Inclusive block scan of one value per thread (Hillis-Steele over LDS): sum, max or sum
+// saturated at `cap` (values in [0, cap], cap < 2^31, so no partial sum overflows 64 bits).
+enum { kScanSum, kScanMax, kScanSatSum };
+template <int kOp>
+__device__ long long block_scan(long long x, long long* buf, long long cap = 0) {
   const int t = threadIdx.x;
   buf[t] = x;
   __syncthreads();
   for (int off = 1; off < PT; off <<= 1) {
-    const int y = t >= off ? buf[t - off] : (kMax ? INT_MIN : 0);
+    const long long y = t >= off ? buf[t - off] : (kOp == kScanMax ? LLONG_MIN : 0);
     __syncthreads();
-    buf[t] = kMax ? max(buf[t], y) : buf[t] + y;
+    long long r;
+    if (kOp == kScanMax) r = max(buf[t], y);
+    else if (kOp == kScanSum) r = buf[t] + y;
+    else r = min(buf[t] + y, cap);
+    buf[t] = r;
     __syncthreads();
   }
-  const int r = buf[t];
+  const long long r = buf[t];
   __syncthreads();
   return r;
 }
 
-__global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu, int n_docs,
-                                                  int n_tokens, int hq, int kind,
-                                                  int4* __restrict__ items, long capacity) {
+// At most one of `cu` (int32, n_docs + 1 bounds) and `lengths` (int64, n_docs) is non-null (both
+// null only when n_docs is 0).
+// Work-group 0 builds the forward plan (and writes cu_out when it is non-null), work-group 1 the
+// backward plan; a null item pointer skips that kind.
+__global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu,
+                                                  const int64_t* __restrict__ lengths, int n_docs,
+                                                  int n_tokens, int hq, int hkv,
+                                                  int4* __restrict__ fwd_items, long fwd_capacity,
+                                                  int4* __restrict__ bwd_items, long bwd_capacity,
+                                                  int32_t* __restrict__ cu_out) {
   __shared__ int s_bound[kPlanMaxDocs + 1];  // clamped, non-decreasing document bounds
   __shared__ int s_tbase[kPlanMaxDocs + 1];  // exclusive prefix of the per-document tile counts
   __shared__ int s_cnt[kBuckets];
-  __shared__ int s_scan[PT];
+  __shared__ long long s_scan[PT];
   const int tid = threadIdx.x;
+  const int kind = blockIdx.x == 0 ? VA_PLAN_FWD : VA_PLAN_BWD;
+  int4* items = kind == VA_PLAN_FWD ? fwd_items : bwd_items;
+  const long capacity = kind == VA_PLAN_FWD ? fwd_capacity : bwd_capacity;
+  if (items == nullptr) return;  // uniform over the work-group
+  const int group = hq / hkv;
 
-  // bound_d = max over d' <= d of min(max(cu[d'], 0), n_tokens): thread runs of DPB bounds, then
-  // a block max-scan of the run maxima.
-  {
+  // Document bounds, DPB per thread.
+  if (lengths != nullptr) {
+    // bound_0 = 0, bound_d = min(sum of the first d lengths (each clamped into [0, N]), N)
+    long long run[DPB];
+    long long s = 0;
+#pragma unroll
+    for (int i = 0; i < DPB; ++i) {
+      const int d = tid * DPB + i;  // run[i] = sum of lengths[tid*DPB .. d - 1]
+      run[i] = s;
+      long long x = (d < n_docs) ? lengths[d] : 0;
+      x = x < 0 ? 0 : (x > n_tokens ? n_tokens : x);
+      s = min(s + x, (long long)n_tokens);
+    }
+    const long long incl = block_scan<kScanSatSum>(s, s_scan, n_tokens);
+    const long long excl = tid > 0 ? s_scan[tid - 1] : 0;
+    (void)incl;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < DPB; ++i) {
+      const int d = tid * DPB + i;
+      if (d <= n_docs) s_bound[d] = (int)min(excl + run[i], (long long)n_tokens);
+    }
+  } else {
+    // bound_d = max over d' <= d of min(max(cu[d'], 0), N)
     int run[DPB];
     int m = 0;
 #pragma unroll
     for (int i = 0; i < DPB; ++i) {
       const int d = tid * DPB + i;
-      int x = d <= n_docs ? cu[d] : 0;
+      int x = (cu != nullptr && d <= n_docs) ? cu[d] : 0;  // no documents: both inputs null
       x = x < 0 ? 0 : (x > n_tokens ? n_tokens : x);
       m = max(m, x);
       run[i] = m;
     }
-    block_scan<true>(m, s_scan);  // s_scan now holds the inclusive prefix maxima
-    const int prev = tid > 0 ? s_scan[tid - 1] : 0;
+    block_scan<kScanMax>(m, s_scan);  // s_scan holds the inclusive prefix maxima
+    const int prev = tid > 0 ? (int)s_scan[tid - 1] : 0;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < DPB; ++i) {
@@ -78,6 +122,8 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   }
   for (int b = tid; b < kBuckets; b += PT) s_cnt[b] = 0;
   __syncthreads();
+  if (cu_out != nullptr && kind == VA_PLAN_FWD)
+    for (int d = tid; d <= n_docs; d += PT) cu_out[d] = s_bound[d];
 
   // Tile counts and their exclusive prefix sum (DPB documents per thread).
   {
@@ -89,7 +135,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       cnt[i] = d < n_docs ? tiles_of(s_bound[d + 1] - s_bound[d]) : 0;
       sum += cnt[i];
     }
-    const int incl = block_scan<false>(sum, s_scan);
+    const int incl = (int)block_scan<kScanSum>(sum, s_scan);
     int run = incl - sum;
 #pragma unroll
     for (int i = 0; i < DPB; ++i) {
@@ -148,7 +194,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       cnt[i] = s_cnt[kBuckets - 1 - (tid * BPT + i)];
       tot += cnt[i];
     }
-    const int incl = block_scan<false>(tot, s_scan);
+    const int incl = (int)block_scan<kScanSum>(tot, s_scan);
     int run = incl - tot;
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
@@ -157,14 +203,23 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
     }
   }
   __syncthreads();
+  // Candidate at sorted position `pos` holds combos pos * Hkv + g (g = GQA group); combo j sits
+  // in column j % 8 of block j / 8, which spans 8 G slots (fewer columns in the last block);
+  // head r of the group goes to row r.
+  const long n_combos = (long)n_cand * hkv;
   for (int c = tid; c < n_cand; c += PT) {
     int doc, t, is_q;
     decode(c, doc, t, is_q);
     const long pos = atomicAdd(&s_cnt[bucket(doc, t, is_q)], 1);
     const int s = s_bound[doc], e = s_bound[doc + 1];
-    for (int h = 0; h < hq; ++h) {
-      const long slot = pos * hq + h;
-      if (slot < capacity) items[slot] = int4{s + t * kTile, e, s, (is_q << 24) | h};
+    for (int g = 0; g < hkv; ++g) {
+      const long combo = pos * hkv + g;
+      const long blk = combo / kXcds, col = combo % kXcds;
+      const long ncols = min((long)kXcds, n_combos - blk * kXcds);
+      for (int r = 0; r < group; ++r) {
+        const long slot = blk * kXcds * group + r * ncols + col;
+        if (slot < capacity) items[slot] = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
+      }
     }
   }
   for (long slot = (long)n_cand * hq + tid; slot < capacity; slot += PT) items[slot] = int4{0, 0, 0, 0};
@@ -172,10 +227,12 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
 
 }  // namespace
 
-hipError_t launch_plan_device(const int32_t* cu, int n_docs, int n_tokens, int hq, int kind,
-                              int32_t* items, long capacity, hipStream_t stream) {
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(PT), 0, stream, cu, n_docs, n_tokens, hq, kind,
-                     (int4*)items, capacity);
+hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
+                              int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
+                              int32_t* bwd_items, long bwd_capacity, int32_t* cu_out,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL(plan_kernel, dim3(2), dim3(PT), 0, stream, cu, lengths, n_docs, n_tokens, hq,
+                     hkv, (int4*)fwd_items, fwd_capacity, (int4*)bwd_items, bwd_capacity, cu_out);
   return hipGetLastError();
 }
 

@@ -83,15 +83,19 @@ struct RopeArgs {
 
 hipError_t launch_fwd(const FwdArgs& a);
 hipError_t launch_bwd(const BwdArgs& a);
-hipError_t launch_bwd_stage(const BwdArgs& a, int stage);  // 0 prepare, 1 main, 2 finish
+hipError_t launch_bwd_stage(const BwdArgs& a, int stage);  // 1 main, 2 finish
 hipError_t launch_rope_fwd(const RopeArgs& a);
 hipError_t launch_rope_bwd(const RopeArgs& a);
 hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t* t_idx,
                             int64_t n_tokens, int heads, int seq, int row_bytes, int mode,
                             hipStream_t stream);
 
-// Device-built plan (plan_device.hip): `capacity` items, real ones first, empty ones after.
-hipError_t launch_plan_device(const int32_t* cu, int n_docs, int n_tokens, int hq, int kind,
-                              int32_t* items, long capacity, hipStream_t stream);
+// Device-built plans (plan_device.hip): from a device cu_seqlens or from device lengths (exactly
+// one non-null); each requested plan (non-null items) is `capacity` items, real ones first, empty
+// ones after; cu_out (nullable) receives the clamped document bounds.
+hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
+                              int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
+                              int32_t* bwd_items, long bwd_capacity, int32_t* cu_out,
+                              hipStream_t stream);
 
 }  // namespace va

@@ -1,95 +1,122 @@
-"""Offload of the tensors a packed-attention layer keeps for its backward to pinned host memory.
+"""Host offload of what a packed-attention layer keeps for its backward.
 
-Keeps the contract the reference's PackedAttention relies on (solution/offload.py:71-73, 86-95,
+The interface is the one the reference's PackedAttention calls (solution/offload.py:71-73, 86-95,
 153-170; used at solution/attention.py:266-274 and 283):
 
     OFFLOADER.begin(device) / OFFLOADER.end()   bracket a forward pass (the caller does this)
-    OFFLOADER.wants(*tensors)  -> bool           offload these tensors?
-    OFFLOADER.save(*tensors)   -> item           start their device-to-host copy
-    OFFLOADER.load(item)       -> tensors        bring them back (bit for bit) on the device
+    OFFLOADER.wants(*tensors)  -> bool           should these tensors be offloaded?
+    OFFLOADER.save(*tensors)   -> handle         hand them over (they may leave the GPU)
+    OFFLOADER.load(handle)     -> tensors        get them back on the GPU, bit for bit
 
-Design for a 288 GB device: the newest `keep_bytes` of saved tensors stay on the GPU (the
-backward needs them first); older items are copied to pinned host memory on a side stream at the
-default priority, and the compute stream waits for a copy before the GPU memory is released. In
-the backward, `load` copies an item back on the side stream and makes the compute stream wait for
-that copy only. Outside begin()/end() nothing is offloaded.
+How this one works. Saved layers form a queue in forward order. While the saved bytes still on
+the GPU exceed KEEP_BYTES, the oldest layer (never the newest: the backward needs that one first)
+is copied to pinned host memory on a side stream that first waits for the compute stream's work
+so far. The device tensors are marked as in use by the side stream (`record_stream`), so the
+caching allocator does not reuse their memory before the copy has read them; the compute stream
+never waits for an eviction. `load` brings a layer back on the side stream into memory allocated
+there, marks it as used by the compute stream, and makes only the compute stream wait for that
+copy. Because the backward visits the layers in reverse, each load also starts bringing back the
+previous evicted layer, so its copy overlaps the current layer's backward. All streams have the
+default priority. Pinned buffers are released through torch's caching host allocator, which holds
+a block until the copies queued on it have finished.
 """
 
 import torch
 
-KEEP_BYTES = 1 << 30  # newest bytes left on the GPU at the end of the forward
+KEEP_BYTES = 1 << 30  # saved bytes allowed to stay on the GPU at the end of a forward pass
 
 
-class _Item:
-    __slots__ = ("tensors", "host", "nbytes", "copied")
+class _Layer:
+    """One save() call: where its tensors are (device list, host list, or a copy on its way back)
+    and the events that order the copies."""
 
-    def __init__(self, tensors):
-        self.tensors = tensors
-        self.host = None
-        self.copied = None
+    __slots__ = ("index", "peers", "on_device", "on_host", "returning", "nbytes", "host_ready",
+                 "device_ready")
+
+    def __init__(self, index, peers, tensors):
+        self.index = index
+        self.peers = peers  # the layers saved in the same forward pass, in order
+        self.on_device = list(tensors)
+        self.on_host = None
+        self.returning = None
         self.nbytes = sum(t.numel() * t.element_size() for t in tensors)
+        self.host_ready = None
+        self.device_ready = None
 
 
 class Offloader:
     def __init__(self):
-        self.active = False
-        self.items = []
-        self.stream = None
-        self.resident = 0
-        self.evict_next = 0
+        self._active = False
+        self._layers = []
+        self._oldest_on_device = 0
+        self._device_bytes = 0
+        self._side = None
 
     def begin(self, device):
-        self.items, self.resident, self.evict_next = [], 0, 0
-        if self.stream is None or self.stream.device != torch.device(device):
-            self.stream = torch.cuda.Stream(device=device)  # default priority
-        self.active = True
+        device = torch.device(device)
+        if self._side is None or self._side.device != device:
+            self._side = torch.cuda.Stream(device=device)
+        self._layers, self._oldest_on_device, self._device_bytes = [], 0, 0
+        self._active = True
 
     def end(self):
-        self.active = False
+        self._active = False
 
     def wants(self, *tensors):
-        return self.active and torch.is_grad_enabled() and all(t.is_cuda for t in tensors)
+        return self._active and torch.is_grad_enabled() and all(t.is_cuda for t in tensors)
 
     def save(self, *tensors):
-        item = _Item(tensors)
-        self.items.append(item)
-        self.resident += item.nbytes
-        while self.resident > KEEP_BYTES and self.evict_next < len(self.items) - 1:
-            old = self.items[self.evict_next]
-            self.evict_next += 1
-            self.resident -= old.nbytes
-            self._to_host(old)
-        return item
+        layer = _Layer(len(self._layers), self._layers, tensors)
+        self._layers.append(layer)
+        self._device_bytes += layer.nbytes
+        while (self._device_bytes > KEEP_BYTES
+               and self._oldest_on_device < len(self._layers) - 1):
+            self._evict(self._layers[self._oldest_on_device])
+            self._oldest_on_device += 1
+        return layer
 
-    def _to_host(self, item):
-        compute = torch.cuda.current_stream()
-        produced = compute.record_event()
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(produced)
-            item.host = []
-            for t in item.tensors:
-                buf = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
-                buf.copy_(t, non_blocking=True)
-                item.host.append(buf)
-            done = self.stream.record_event()
-        compute.wait_event(done)  # the GPU copy is freed in compute-stream order after this
-        item.tensors = None
+    def _evict(self, layer):
+        compute = torch.cuda.current_stream(self._side.device)
+        self._side.wait_stream(compute)
+        with torch.cuda.stream(self._side):
+            host = []
+            for t in layer.on_device:
+                h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+                h.copy_(t, non_blocking=True)
+                t.record_stream(self._side)
+                host.append(h)
+            layer.host_ready = self._side.record_event()
+        layer.on_host, layer.on_device = host, None
+        self._device_bytes -= layer.nbytes
 
-    def load(self, item):
-        if item.tensors is not None:
-            tensors, item.tensors = item.tensors, None
+    def _bring_back(self, layer):
+        """Queue the host-to-device copy of an evicted layer on the side stream."""
+        compute = torch.cuda.current_stream(self._side.device)
+        with torch.cuda.stream(self._side):
+            self._side.wait_event(layer.host_ready)
+            back = []
+            for h in layer.on_host:
+                d = torch.empty(h.shape, dtype=h.dtype, device=self._side.device)
+                d.copy_(h, non_blocking=True)
+                d.record_stream(compute)
+                back.append(d)
+            layer.device_ready = self._side.record_event()
+        layer.returning = back
+
+    def load(self, layer):
+        if layer.on_device is not None:  # never left the GPU
+            tensors, layer.on_device = layer.on_device, None
             return tensors
-        compute = torch.cuda.current_stream()
-        restored = [torch.empty(h.shape, dtype=h.dtype, device=compute.device) for h in item.host]
-        free = compute.record_event()
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(free)
-            for gpu, host in zip(restored, item.host):
-                gpu.copy_(host, non_blocking=True)
-            ready = self.stream.record_event()
-        compute.wait_event(ready)
-        item.host = None
-        return restored
+        if layer.returning is None:
+            self._bring_back(layer)
+        torch.cuda.current_stream(self._side.device).wait_event(layer.device_ready)
+        tensors, layer.returning, layer.on_host = layer.returning, None, None
+        # the backward runs in reverse: start bringing back the layer saved before this one
+        if layer.index > 0:
+            earlier = layer.peers[layer.index - 1]
+            if earlier.on_host is not None and earlier.returning is None:
+                self._bring_back(earlier)
+        return tensors
 
 
 OFFLOADER = Offloader()

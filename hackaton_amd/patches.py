@@ -26,7 +26,7 @@ def patch_qwen2_attention():
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
                 **kwargs):
         packed = kwargs.pop("packed", None)
-        if packed is None:  # not the packed training step: the original code
+        if packed is None:  # an ordinary call (generation, eval, padded batches): unchanged
             return original(self, hidden_states, position_embeddings, attention_mask,
                             past_key_values, **kwargs)
         b_idx, t_idx, batch, seq, lengths = packed
@@ -34,12 +34,12 @@ def patch_qwen2_attention():
         config = self.config
         q, k, v = (self.q_proj(hidden_states), self.k_proj(hidden_states),
                    self.v_proj(hidden_states))
-        if lengths is not None:  # right padded: per-sequence attention on the packed rows
+        if lengths is not None:  # documents are contiguous row blocks: attend on the rows
             attn = packed_attention(q, k, v, cos, sin, b_idx, t_idx, seq,
                                     config.num_attention_heads, config.num_key_value_heads,
                                     lengths, self.scaling)
             return self.o_proj(attn), None
-        # otherwise the padded layout and the caller's mask
+        # lengths unknown (e.g. left padding): rebuild the padded batch, use the caller's mask
         query, key, value = qkv_rotate(q, k, v, cos, sin, b_idx, t_idx, batch, seq,
                                        config.num_attention_heads, config.num_key_value_heads,
                                        True)

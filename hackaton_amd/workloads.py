@@ -116,18 +116,30 @@ def algorithmic_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
     return fwd + bwd
 
 
-def backward_main_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
-    """HBM bytes the backward's main kernel must move: reads q, dO, O, k, v, lse; writes dq and the
-    per-query-head dK/dV partials (or dK/dV themselves when Hq == Hkv)."""
-    return n_tokens * (6 * hq * d * elem + 2 * hkv * d * elem + 4 * hq)
+def backward_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
+    """HBM bytes one attention backward must move at least: reads q, k, v, O, dO and lse (and the
+    row statistic delta, counted like lse), writes dq, dk and dv at their own widths (dK/dV have
+    Hkv heads: the GQA sum is part of the backward)."""
+    return n_tokens * ((hq + 2 * hkv) * d * elem + 2 * hq * d * elem + 8 * hq
+                       + (hq + 2 * hkv) * d * elem)
 
 
-def gqa_sum_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
-    """HBM bytes of the backward's GQA reduction: reads the dK/dV partials, writes dK/dV."""
+def partial_write_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
+    """Bytes of per-query-head dK/dV partials one backward writes (and the GQA sum reads back)
+    when the query heads of a group are split over work items: an intermediate of this
+    implementation, not algorithmic traffic."""
     if hq == hkv:
         return 0
-    return n_tokens * 2 * (hq + hkv) * d * elem
+    return n_tokens * 2 * hq * d * elem
 
 
 def forward_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
     return n_tokens * ((hq + 2 * hkv) * d * elem + hq * d * elem + 4 * hq)
+
+
+def gqa_sum_bytes(n_tokens, hq, hkv, elem=2, d=HEAD_DIM):
+    """HBM bytes a separate GQA reduction moves: reads the per-head dK/dV partials, writes dK/dV
+    (the dK/dV writes are algorithmic; the partial reads are not)."""
+    if hq == hkv:
+        return 0
+    return n_tokens * 2 * (hq + hkv) * d * elem

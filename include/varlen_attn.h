@@ -13,7 +13,11 @@
  *   lse             (Hq, N)        fp32, natural-log log-sum-exp of each query row
  *   cu_seqlens      (n_docs + 1)   int32 host array, cu[0] = 0, non-decreasing; document i is
  *                                  rows [cu[i], cu[i+1]) of the packed token axis
- *   work items      int32 x 4 each, built on the host by va_plan_build and copied to the device
+ *   work items      int32 x 4 each in device memory: built on the host by va_plan_build (and
+ *                   copied to the device by the caller) or on the device by va_plan_build_device.
+ *                   The kernels skip an item whose head is not below Hq or whose rows do not lie
+ *                   in [0, total_tokens), so a plan made for other sizes cannot write out of
+ *                   bounds (it computes nothing useful either).
  *
  * Reference interfaces replaced (mergentlegen/hackaton, solution/attention.py):
  *   va_plan_build       _cu_seqlens (195-209) + the tile walk inside the aten kernel
@@ -49,7 +53,7 @@ enum {
 enum { VA_F16 = 0, VA_BF16 = 1, VA_F32 = 2 };
 enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1 };
 enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
-enum { VA_BWD_PREPARE = 0, VA_BWD_MAIN = 1, VA_BWD_FINISH = 2 };
+enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2 };
 
 const char* va_last_error(void);
 int32_t va_abi_version(void);
@@ -83,6 +87,22 @@ int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs, int64
                          int32_t hq, int32_t hkv, int32_t kind, int32_t* items_device,
                          int64_t capacity, void* stream);
 
+/* The same plans straight from the per-document lengths (int64, as a mask's row sums give them):
+ * one launch builds cu_seqlens (into cu_seqlens_out, n_docs + 1 int32, when it is non-NULL), the
+ * forward plan and the backward plan (either item pointer may be NULL to skip that kind). Each
+ * length is clamped into [0, n_tokens] and the bounds saturate at n_tokens.
+ * Replaces: lengths.tolist() at solution/packed.py:170-172 and _cu_seqlens at
+ * solution/attention.py:195-209, on the device. */
+int va_plan_build_device_lengths(const int64_t* lengths_device, int32_t n_docs, int64_t n_tokens,
+                                 int32_t hq, int32_t hkv, int32_t* fwd_items_device,
+                                 int64_t fwd_capacity, int32_t* bwd_items_device,
+                                 int64_t bwd_capacity, int32_t* cu_seqlens_out, void* stream);
+
+/* Capture id of the stream's active graph capture, 0 when the stream is not capturing. A utility
+ * with no counterpart in the reference: callers that cache device plans across layers key the
+ * cache on it, so that a plan built inside one capture is reused only inside that capture. */
+int va_stream_capture_id(void* stream, uint64_t* capture_id);
+
 /* ---- attention forward ------------------------------------------------------------------------
  * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row;
  * scale must be finite and > 0 (D^-0.5 in the reference).
@@ -107,9 +127,10 @@ int va_bwd(const void* dout, const void* q, const void* k, const void* v, const 
            int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype, void* dq,
            void* dk, void* dv, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* The same backward in its stages, for callers that time or overlap them separately: prepare
- * (nothing to do in this implementation), main (dQ and the per-head dK/dV partials), finish (the
- * GQA sums into dk/dv; nothing when they are NULL or Hq == Hkv). Same arguments as va_bwd.
+/* The same backward in its two stages, for callers that time or overlap them separately:
+ * VA_BWD_MAIN (dQ and the per-head dK/dV partials) and VA_BWD_FINISH (the GQA sums into dk/dv;
+ * nothing when they are NULL or Hq == Hkv). Any other stage value is VA_EINVAL. Same arguments
+ * as va_bwd.
  * Replaces: the same reference call as va_bwd (solution/attention.py:230-232). */
 int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k, const void* v,
                  const void* out, const float* lse, const int32_t* items, int64_t n_items,
@@ -124,7 +145,8 @@ int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k, 
  * VA_LAYOUT_PADDED writes (B, H, seq, D) (caller zero-fills). expand=1 writes K/V for all `heads`
  * (reference qkv_rotate semantics); expand=0 keeps kv_heads (GQA-native attention input).
  * Backward: the inverse rotation (and the sum of the G copies when expand=1); dq/dk/dv read in
- * in_dtype from `layout`, written (N, H*D) in out_dtype.
+ * in_dtype from `layout`, written (N, H*D) in out_dtype. Every tensor base must be 16-byte aligned
+ * and the cos/sin strides (in elements) non-negative multiples of 4: each lane moves 16 bytes.
  * Replaces: solution/attention.py:36-134 (qkv_kernel modes 0 and 1). */
 int va_rope_fwd(const void* q, const void* k, const void* v, const float* cos, const float* sin,
                 int64_t cos_batch_stride, int64_t cos_seq_stride, const int32_t* b_idx,

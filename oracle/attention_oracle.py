@@ -26,8 +26,9 @@ retype its formula: torch's own scaled_dot_product_attention (forward and autogr
 the reference test's padded masked-SDPA construction (test_attention.py:95-106), transformers'
 apply_rotary_pos_emb/repeat_kv, brute-force pure-Python loops, closed forms (length-1 documents,
 constant keys), invariants (rows of P sum to 1, rowsum(dS) = 0) and central finite differences of
-the forward for the backward. `attention_forward_logits_lse` has no check beyond the closed form
-and scipy's logsumexp, which pin it.
+the forward for the backward. The log-sum-exp output of `attention_forward` is pinned by the
+closed form of length-1 documents, by torch.logsumexp over the masked logits and by a
+brute-force loop.
 
 All arithmetic is in the dtype requested (float64 for checking, float32 for the CPU baseline).
 Layouts: q (N, Hq, D), k/v (N, Hkv, D), o (N, Hq, D), lse (Hq, N).

@@ -42,12 +42,14 @@ def test_above_ridge_is_mfma_bound():
 def test_config2_kernels_sit_below_the_ridge():
     lengths = wl.config_lengths(2)
     cfg = wl.CONFIGS[2]
-    n = sum(lengths)
-    fwd = wl.forward_flops(lengths, cfg["hq"]) / wl.forward_bytes(n, cfg["hq"], cfg["hkv"])
-    bwd = 2.5 * wl.forward_flops(lengths, cfg["hq"]) / wl.backward_main_bytes(
-        n, cfg["hq"], cfg["hkv"])
+    models = bench.kernel_models(lengths, cfg["hq"], cfg["hkv"])
     ridge = 2516.6e12 / 8000e9
-    assert fwd < ridge and bwd < ridge
+    for name in ("fwd_kernel", "bwd_kernel"):
+        assert models[name]["flops"] / models[name]["bytes"] < ridge
+    # the backward's arithmetic intensity at 4 x 512 tokens: 8.07 GFLOP over 29.56 MB
+    bwd = models["bwd_kernel"]
+    assert bwd["bytes"] == 2048 * 14432
+    assert bwd["flops"] / bwd["bytes"] == pytest.approx(273.0, abs=0.5)
 
 
 def test_causal_pairs_match_mask_count():
@@ -62,11 +64,15 @@ def test_byte_models_by_hand():
     # Hq=12, Hkv=2, D=128, fp16, one token:
     #   q 12*128*2 = 3072, k+v 2*2*128*2 = 1024, O 3072, lse 12*4 = 48.
     assert wl.forward_bytes(1, 12, 2) == 3072 + 1024 + 3072 + 48
-    #   backward main: q, dO, O (3*3072), k+v (1024), lse (48), dq + dK/dV partials (3*3072).
-    assert wl.backward_main_bytes(1, 12, 2) == 6 * 3072 + 1024 + 48
-    #   GQA reduction: reads 2*12 partial heads, writes 2*2 heads.
+    #   backward: reads q (3072), k+v (1024), O and dO (2*3072), lse and delta (2*48); writes
+    #   dq (3072) and dk+dv at Hkv width (1024).
+    assert wl.backward_bytes(1, 12, 2) == 3072 + 1024 + 2 * 3072 + 96 + 3072 + 1024 == 14432
+    assert wl.forward_bytes(1, 12, 2) + wl.backward_bytes(1, 12, 2) == 21648
+    assert wl.algorithmic_bytes(7, 12, 2) == 7 * 21648
+    #   per-head dK/dV partials: 2 tensors x 12 heads; GQA reduction reads them, writes 2*2 heads.
+    assert wl.partial_write_bytes(1, 12, 2) == 24 * 128 * 2
     assert wl.gqa_sum_bytes(1, 12, 2) == (24 + 4) * 128 * 2
-    assert wl.gqa_sum_bytes(5, 4, 4) == 0
+    assert wl.gqa_sum_bytes(5, 4, 4) == 0 and wl.partial_write_bytes(5, 4, 4) == 0
 
 
 def test_forward_flops_by_hand():
@@ -90,3 +96,48 @@ def test_more_than_one_gpu_is_refused():
     assert p.returncode == 2
     msg = json.loads(p.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+def test_median_per_launch():
+    assert bench.median_us([1.0, 3.0, 2.0], 28) == pytest.approx(2.0e3 / 28)
+
+
+@pytest.mark.parametrize("lengths,hq,hkv", [([9, 1, 4], 4, 2), ([6, 3], 2, 2)])
+def test_cpu_baseline_constructions_match_the_oracle(lengths, hq, hkv):
+    """Both CPU-baseline constructions (the reference test's padded tril & real mask and
+    per-document is_causal) compute the oracle's outputs and gradients."""
+    import torch
+
+    from oracle import attention_oracle as orc
+
+    q, k, v, do = wl.make_inputs(lengths, hq, hkv, torch.float32, seed=4)
+    grad = do.reshape(do.shape[0], -1)
+    cu = orc.cu_seqlens_from_lengths(lengths)
+    f64 = [t.double().numpy() for t in (q, k, v, do)]
+    o_ref, lse = orc.attention_forward(f64[0], f64[1], f64[2], cu, 0.3)
+    refs = orc.attention_backward(f64[0], f64[1], f64[2], o_ref, lse, f64[3], cu, 0.3)
+    for fn in (bench.sdpa_padded_call, bench.sdpa_per_document_call):
+        out, grads = fn(q, k, v, grad, lengths, 0.3)
+        np.testing.assert_allclose(out.numpy().reshape(o_ref.shape), o_ref, atol=1e-5)
+        for mine, ref in zip(grads, refs):
+            np.testing.assert_allclose(mine.numpy(), ref, atol=1e-5)
+
+
+def test_cpu_baseline_reports_cores_and_model(monkeypatch):
+    """The CPU leg states the threads it used, the logical CPU count and the CPU model; run on a
+    tiny configuration so that the test stays fast."""
+    import torch
+
+    monkeypatch.setitem(wl.CONFIGS, 99, dict(name="tiny", hq=4, hkv=2, dtype="float16",
+                                             qk_scale=1.0))
+    real = wl.config_lengths
+    monkeypatch.setattr(wl, "config_lengths", lambda c, seed=0: [5, 3] if c == 99 else real(c))
+    threads = torch.get_num_threads()
+    try:
+        r = bench.cpu_baseline((99,))
+    finally:
+        torch.set_num_threads(threads)
+    assert r["unit"] == "TFLOP/s" and r["value"] > 0 and r["cores"] >= 1
+    assert r["cpu_model"] and r["logical_cpus"] >= 1
+    row = r["configs"]["config99"]
+    assert set(row) >= {"padded_masked", "per_document_causal", "best_tflops"}
