@@ -39,6 +39,9 @@ SIGNATURES = {
     "va_bwd_workspace_layout": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64, _pi64]),
     "va_bwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32,
                               _i32, _p, _p, _p, _p, _i64, _p]),
+    "va_bwd_noalloc_max_bytes": (_i64, []),
+    "va_bwd_noalloc": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
+                                      _f32, _i32, _p, _p, _p, _p]),
     "va_bwd_stage": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                     _f32, _i32, _p, _p, _p, _p, _i64, _p]),
     "va_rope_fwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i32,

@@ -92,13 +92,13 @@ extern "C" int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t
   return VA_OK;
 }
 
-namespace {
+namespace va {
 
-int bwd_common(int32_t stage, const void* dout, const void* q, const void* k, const void* v,
-               const void* out, const float* lse, const int32_t* items, int64_t n_items,
-               int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim, float scale,
-               int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
-               int64_t workspace_bytes, void* stream) {
+int bwd_checked(int32_t stage, const void* dout, const void* q, const void* k, const void* v,
+                const void* out, const float* lse, const int32_t* items, int64_t n_items,
+                int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim, float scale,
+                int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   int rc = check_attn_shape(total_tokens, hq, hkv, head_dim);
   if (rc) return rc;
   if ((rc = check_dtype16(dtype))) return rc;
@@ -128,15 +128,15 @@ int bwd_common(int32_t stage, const void* dout, const void* q, const void* k, co
   return e == hipSuccess ? VA_OK : hip_fail(e, "va_bwd launch");
 }
 
-}  // namespace
+}  // namespace va
 
 extern "C" int va_bwd(const void* dout, const void* q, const void* k, const void* v,
                       const void* out, const float* lse, const int32_t* items, int64_t n_items,
                       int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim, float scale,
                       int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
                       int64_t workspace_bytes, void* stream) {
-  return bwd_common(-1, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, head_dim,
-                    scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
+  return va::bwd_checked(-1, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
+                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
 }
 
 extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k,
@@ -147,8 +147,8 @@ extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, cons
                             int64_t workspace_bytes, void* stream) {
   if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH)
     return va::fail(VA_EINVAL, "va_bwd_stage: stage %d", stage);
-  return bwd_common(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
-                    head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
+  return va::bwd_checked(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
+                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
 }
 
 namespace {

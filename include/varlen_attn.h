@@ -127,6 +127,19 @@ int va_bwd(const void* dout, const void* q, const void* k, const void* v, const 
            int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype, void* dq,
            void* dk, void* dv, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The same backward for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Same inputs and outputs as va_bwd, no workspace: the dK/dV partials live in a static
+ * device array of the library (va_bwd_noalloc_max_bytes() = 64 MiB per GPU, held until the
+ * process ends), so total_tokens * Hq must not exceed 131072 at head_dim 128 (VA_ECAPACITY
+ * otherwise, before any launch); dk and dv must be given. Calls nothing that allocates. Calls
+ * that overlap on one GPU (two streams or two threads) race on the shared array. */
+int64_t va_bwd_noalloc_max_bytes(void);
+int va_bwd_noalloc(const void* dout, const void* q, const void* k, const void* v, const void* out,
+                   const float* lse, const int32_t* items, int64_t n_items, int64_t total_tokens,
+                   int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype, void* dq,
+                   void* dk, void* dv, void* stream);
+
 /* The same backward in its two stages, for callers that time or overlap them separately:
  * VA_BWD_MAIN (dQ and the per-head dK/dV partials) and VA_BWD_FINISH (the GQA sums into dk/dv;
  * nothing when they are NULL or Hq == Hkv). Any other stage value is VA_EINVAL. Same arguments
