@@ -242,11 +242,9 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
     dq = torch.empty_like(query)
     if outputs:
         dk, dv = torch.empty_like(key), torch.empty_like(value)
-        ws, offs = (bwd_workspace(n, hq, hkv, query.device) if hq != hkv
-                    else (torch.empty(0, dtype=torch.uint8, device=query.device), [0, 0]))
     else:
         dk = dv = None
-        ws, offs = bwd_workspace(n, hq, hkv, query.device)
+    ws, offs = bwd_workspace(n, hq, hkv, query.device)
     check(lib().va_bwd(_ptr(grad), _ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
                        _ptr(plan.bwd_items), plan.n_bwd, n, hq, hkv, d, float(scale), dtype,
                        _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws) if ws.numel() else None,

@@ -576,7 +576,7 @@ def test_kernels_skip_items_of_a_plan_for_other_sizes():
                          plan_big.fwd_items.data_ptr(), plan_big.n_fwd, n, hq_small, hkv, 128,
                          SCALE, 0, att._stream()), "va_fwd")
     qb, dq = canaried((n, hq_small, 128), torch.float16)
-    ws_bytes = 2 * n * hq_small * 128 * 2 + 512
+    ws_bytes = att.bwd_workspace(n, hq_small, hkv, q.device)[0].numel()
     wb, ws = canaried((ws_bytes,), torch.uint8)
     kb, dk = canaried((n, hkv, 128), torch.float16)
     vb, dv = canaried((n, hkv, 128), torch.float16)
