@@ -2,10 +2,11 @@
 //
 // One work-group = one work item of the plan: 128 queries (4 strips of 32) of one document and one
 // query head, run by 8 waves in two halves. Half h (waves 4h .. 4h + 3) processes the key tiles
-// t = h, h + 2, h + 4, ... (64 keys each) for the 4 query strips, so two waves share each SIMD:
-// one wave's MFMAs overlap the other's softmax, LDS waits and barrier skew, and the key range of
-// the work item is split in two. At the end the halves swap their unnormalised partial O through
-// LDS and publish (m, l); each half finishes 64 of the 128 columns, half 0 also the log-sum-exp.
+// t = h, h + 2, h + 4, ... (64 keys each) for the 4 query strips, so two waves share each SIMD
+// and the key range of the work item is split in two. The halves run out of phase: half 1
+// computes S^T of its next tile at the end of a pair, so a pair starts with half 0's S^T MFMAs
+// beside half 1's softmax. At the end the halves swap their unnormalised partial O through LDS
+// and publish (m, l); each half finishes 64 of the 128 columns, half 0 also the log-sum-exp.
 //
 // Per wave: Q (copied once into LDS, read back as each lane's row) stays in registers as the MFMA B
 // operand; S^T = K Q^T (v_mfma_f32_32x32x16) puts one query per lane, so the online softmax is
@@ -77,10 +78,9 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   // lands in chunk slot i & 15 of row i >> 4 of the group, so it fetches logical chunk
   // (i & 15) ^ swz16(row). Loads are bounded at the document end: rows past it read as zeros
   // (masked keys, zero P).
-  // Only the waves of half 1 copy: a copy instruction stalls its wave on the memory queue until
-  // the CU takes it (64 KB per pair enter the CU at ~80 B/clk), and with one copying wave per
-  // SIMD the other one starts its MFMAs at once, so the two run out of phase. Wave (1, s) moves
-  // row groups g = 2 s + j and 2 (s + 4) + j (j = 0, 1) of each tile, 4 rows per instruction.
+  // One half copies (half 1 the first pair, half 0 the others): a copy instruction stalls its
+  // wave on the memory queue until the CU takes it. Wave (h, s) moves row groups g = 2 s + j and
+  // 2 (s + 4) + j (j = 0, 1) of each tile, 4 rows per instruction.
   const int ws = __builtin_amdgcn_readfirstlane(strip);
   int coff[4];  // [jj]: bytes from the tile's first row, row group 2 (s + 4 (jj >> 1)) + (jj & 1)
 #pragma unroll
@@ -88,25 +88,29 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
     const int r = 4 * (2 * (strip + 4 * (jj >> 1)) + (jj & 1)) + (lane >> 4);
     coff[jj] = (r * (int)kvrow + 8 * ((lane & 15) ^ swz16(r))) * 2;
   }
-  // All 16 copies of a wave are issued together at the start of a pair (stalling between MFMAs
-  // costs more). Copy (t, x, jj): tile t of the pair, tensor x (K, V), row group jj.
+  // Copy of key tile `t` of tensor x (K, V) into the tile slot at LDS byte address `dst`.
+  auto copy_tile = [&](int t, int x, uint32_t dst) {
+    const int row0 = doc_start + t * BN;
+    const long base = (long)row0 * kvrow + kvh * D;
+    const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
+    const u32x4 r = make_rsrc4((x ? v : k) + base, bytes);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      dma16_opaque(r, dst + ((8 * (ws + 4 * (jj >> 1)) + 4 * (jj & 1)) * D) * 2, coff[jj]);
+  };
+  // The stage of pair p holds K0, V0, V1 of the pair and K1 of the NEXT pair (slots K0, V0, K1,
+  // V1): half 1 computes S^T of its next tile at the end of a pair, after its O^T += V^T P^T, so
+  // that at the start of the following pair its softmax (VALU) runs while half 0 computes its S^T
+  // (MFMA) on the same SIMD. The K1 copy is left out when that tile does not exist.
+  // In the loop, half 0 issues the copies of the next pair, after its S^T MFMAs: the copy
+  // instructions stall the issuing wave while the CU takes 64 KB per pair (~1,100 cycles at the
+  // CU's fill rate), and half 0 has that slack (half 1 carries the S^T of the next tile).
   auto copy_pair = [&](int p, int stage) {
-    if (half != 1) return;
     const uint32_t dst = lds_addr(smem + stage * PAIR);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int row0 = doc_start + (2 * p + t) * BN;
-      const long base = (long)row0 * kvrow + kvh * D;
-      const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
-      const u32x4 r[2] = {make_rsrc4(k + base, bytes), make_rsrc4(v + base, bytes)};
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          dma16_opaque(r[x],
-                       dst + ((2 * t + x) * TILE + (8 * (ws + 4 * (jj >> 1)) + 4 * (jj & 1)) * D) * 2,
-                       coff[jj]);
-    }
+    copy_tile(2 * p, 0, dst);
+    copy_tile(2 * p, 1, dst + TILE * 2);
+    copy_tile(2 * p + 1, 1, dst + 3 * TILE * 2);
+    if (2 * p + 3 < n_tiles) copy_tile(2 * p + 3, 0, dst + 2 * TILE * 2);
   };
 
   // Per-lane LDS read offsets (halfs) inside a tile. K (A operand of S^T): row perm32(l32)
@@ -134,12 +138,11 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // One 64-key tile for this wave: S^T, mask, online softmax, O^T += V^T P^T.
-  auto tile = [&](int stage, int t) {
-    const int kv0 = doc_start + t * BN;
-    const lds_u16* kb = smem + stage * PAIR + 2 * half * TILE;
-    // S^T: 16 MFMAs over (kk, b), each K operand read from LDS 4 MFMAs ahead of its use.
-    f32x16 s[2] = {f32x16{}, f32x16{}};
+  // S^T of one 64-key tile (K at `kb`): 16 MFMAs over (kk, b), each K operand read from LDS 4
+  // MFMAs ahead of its use.
+  auto s_tile = [&](const lds_u16* kb, f32x16(&s)[2]) {
+    s[0] = f32x16{};
+    s[1] = f32x16{};
     u32x4 ka[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ka[i] = ld128(kb + koff[i >> 1] + 32 * (i & 1) * D);
@@ -156,6 +159,11 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
       VA_SCHED(kSchedDsRead, 1);
     }
     VA_SCHED(kSchedMfma, 4);
+  };
+  // The rest of a tile for this wave: mask, online softmax, O^T += V^T P^T (V of the tile in the
+  // stage's V slot of this half).
+  auto pv_tile = [&](int stage, int t, f32x16(&s)[2]) {
+    const int kv0 = doc_start + t * BN;
     // The first V^T operands of O^T += V^T P^T, read while the softmax runs.
     const lds_u16* vb = smem + stage * PAIR + (2 * half + 1) * TILE;
     auto v_read = [&](int i) {  // i = (b, c, db) in MFMA order
@@ -235,7 +243,8 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
                    (r * (int)qrow + h * D + 8 * ((lane & 15) ^ swz16(r))) * 2);
     }
   }
-  copy_pair(0, 0);
+  if (half == 1) copy_pair(0, 0);
+  if (half == 1 && 1 < n_tiles) copy_tile(1, 0, lds_addr(smem + PAIR + 2 * TILE));
   wait_vmcnt<0>();
   __syncthreads();
   {
@@ -245,15 +254,39 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   }
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
-  __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
-  for (int p = 0; p < n_pairs; ++p) {
-    const int stage = p & 1;
-    if (p + 1 < n_pairs) copy_pair(p + 1, stage ^ 1);
-    const int t = 2 * p + half;
-    // Tiles entirely past this strip's diagonal are skipped (their P would be all zero).
-    if (t < n_tiles && doc_start + t * BN <= wq0 + 31) tile(stage, t);
-    wait_vmcnt<0>();  // this wave's copies of the next pair have landed in LDS
-    __syncthreads();
+  // Tiles entirely past this strip's diagonal are skipped (their P would be all zero).
+  // (wave-uniform: the strip's first query through readfirstlane, so the branches are scalar)
+  const int wq0_u = __builtin_amdgcn_readfirstlane(wq0);
+  auto visible = [&](int t) { return t < n_tiles && doc_start + t * BN <= wq0_u + 31; };
+  // The halves run separate loops (same barriers), so that half 1's S^T carried across a
+  // barrier takes no registers in half 0's loop.
+  if (half == 0) {
+    __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
+    for (int p = 0; p < n_pairs; ++p) {
+      const int stage = p & 1;
+      const int t = 2 * p;
+      if (visible(t)) {
+        f32x16 s[2];
+        s_tile(smem + stage * PAIR, s);
+        if (p + 1 < n_pairs) copy_pair(p + 1, stage ^ 1);
+        pv_tile(stage, t, s);
+      } else if (p + 1 < n_pairs) {
+        copy_pair(p + 1, stage ^ 1);
+      }
+      wait_vmcnt<0>();  // this wave's copies of the next pair have landed in LDS
+      __syncthreads();
+    }
+  } else {
+    f32x16 s[2];
+    if (visible(1)) s_tile(smem + PAIR + 2 * TILE, s);
+    __syncthreads();  // every wave holds its Q, half 1 its first S^T, before stage 1 is reused
+    for (int p = 0; p < n_pairs; ++p) {
+      const int stage = p & 1;
+      const int t = 2 * p + 1;
+      if (visible(t)) pv_tile(stage, t, s);
+      if (visible(t + 2)) s_tile(smem + stage * PAIR + 2 * TILE, s);  // K1 of pair p + 1
+      __syncthreads();
+    }
   }
 
   // Merge the two halves through LDS (same lane order: the partner wave holds the same (query,
