@@ -188,14 +188,17 @@ def sdpa_per_document_call(q, k, v, grad, lengths, scale):
     return out.detach(), [x.grad for x in leaves]
 
 
-def time_cpu(fn, args, warmup=2, reps=5):
+def time_cpu(fn, args, warmup=2, reps=5, budget_s=2.5):
+    """Best of at least `reps` timed calls, repeated until `budget_s` seconds of timed work (so the
+    whole CPU sample is ~10 s of CPU work: 2 configurations x 2 constructions)."""
     for _ in range(warmup):
         fn(*args)
-    best = math.inf
-    for _ in range(reps):
+    best, spent, n = math.inf, 0.0, 0
+    while n < reps or spent < budget_s:
         t0 = time.perf_counter()
         fn(*args)
-        best = min(best, time.perf_counter() - t0)
+        dt = time.perf_counter() - t0
+        best, spent, n = min(best, dt), spent + dt, n + 1
     return best
 
 
@@ -233,7 +236,8 @@ def cpu_baseline(configs=(1, 2)):
             "kind": "reference",
             "sample": (f"torch CPU scaled_dot_product_attention fp32 fwd+autograd bwd, GQA via "
                        f"enable_gqa, padded tril&real mask (solution/test_attention.py:95-106) and "
-                       f"per-document is_causal, faster of the two, min of 5 after 2 warm-ups, "
+                       f"per-document is_causal, faster of the two, best of >= 5 calls and "
+                       f">= 2.5 s per construction after 2 warm-ups, "
                        f"one layer call of configuration {configs[-1]}'s shape; configuration 1 "
                        f"also timed; {threads} threads of {os.cpu_count()} logical CPUs, "
                        f"{cpu_model()}; {total:.1f} s of CPU work"),
