@@ -4,7 +4,8 @@
 //
 // One launch, one 1024-thread work-group per plan kind (forward, backward). Each work-group takes
 // the document bounds (from a device cu_seqlens, or from device lengths through a saturating
-// prefix sum), clamps them into [0, n_tokens] and makes them non-decreasing; counts each
+// prefix sum), clamps them into [0, n_tokens], makes them non-decreasing and ends the last
+// document at n_tokens (rows past the lengths' sum join it); counts each
 // document's tiles and prefix-sums the counts in LDS; sorts the tile candidates by the host
 // planner's work measure (counting sort, buckets of 8), longest first; and writes one item per
 // (candidate, query head) in the host planner's XCD layout: every candidate is Hkv combos (one
@@ -120,6 +121,10 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       if (d <= n_docs) s_bound[d] = max(prev, run[i]);
     }
   }
+  // Every row belongs to a document: rows past the last bound (lengths summing below n_tokens)
+  // join the last document, so no output or gradient row is left unwritten.
+  __syncthreads();  // every bound written before the last one is replaced
+  if (tid == 0 && n_docs > 0) s_bound[n_docs] = n_tokens;
   for (int b = tid; b < kBuckets; b += PT) s_cnt[b] = 0;
   __syncthreads();
   if (cu_out != nullptr && kind == VA_PLAN_FWD)

@@ -80,8 +80,10 @@ int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t
  * ceil(n_tokens / 128) + n_docs tiles per query head, twice that for VA_PLAN_BWD.
  * va_plan_build_device writes exactly `capacity` items (int32 x 4) to device memory: the real
  * ones longest first, then empty items that va_fwd / va_bwd skip, so the kernels take n_items =
- * capacity. Document bounds are clamped into [0, n_tokens] and made non-decreasing on the device.
- * n_docs <= 8192. */
+ * capacity. Document bounds are clamped into [0, n_tokens] and made non-decreasing on the device,
+ * and the last document ends at n_tokens: rows past the lengths' sum (which the host planner
+ * rejects, and which a device plan cannot report without a host read) join the last document, so
+ * every output and gradient row is written. n_docs <= 8192. */
 int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t kind, int64_t* capacity);
 int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs, int64_t n_tokens,
                          int32_t hq, int32_t hkv, int32_t kind, int32_t* items_device,

@@ -471,6 +471,28 @@ def test_device_lengths_run_without_host_reads_and_match_host_lengths():
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("lengths,n_rows", [([334, 200, 100], 700), ([100, 0, 50, 0], 230)])
+def test_device_lengths_summing_below_n_extend_the_last_document(lengths, n_rows):
+    """Device lengths whose sum falls short of the rows cannot be checked without a host read (the
+    host path raises ValueError): the device plan ends the last document at N, so every output and
+    gradient row is written, bitwise as host lengths whose last document takes the rest."""
+    hq, hkv = 12, 2
+    banner("device lengths below N", lengths, n_rows)
+    extended = list(lengths)
+    extended[-1] += n_rows - sum(lengths)
+    q, k, v, do = wl.make_inputs([x for x in extended if x], hq, hkv, torch.float16, seed=9)
+    assert q.shape[0] == n_rows
+    with pytest.raises(ValueError):
+        run_varlen(q, k, v, do, lengths)
+    host = run_varlen(q, k, v, do, extended)
+    qd, kd, vd = (t.cuda().requires_grad_() for t in (q, k, v))
+    out = att.varlen_attention(qd, kd, vd, torch.tensor(lengths, device="cuda"), SCALE)
+    out.backward(do.cuda().reshape(out.shape))
+    torch.cuda.synchronize()
+    for a, b in zip(host, (out.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu())):
+        assert torch.equal(a, b)
+
+
 def test_packed_attention_save_policies_agree_bitwise():
     """Keeping O / lse for the backward ("outputs") gives the same output and gradients, bit for
     bit, as recomputing the forward in the backward ("inputs", the reference's choice), and keeps
