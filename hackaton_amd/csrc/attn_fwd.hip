@@ -350,9 +350,244 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   else merge(std::integral_constant<int, 0>{});
 }
 
+// --------------------------------------------------------------------------------------------
+// Forward for many work items: 4 waves per work item (one per query strip, each over all of the
+// item's key tiles), 64 KB of LDS, so two work-groups share a CU. The two waves of a SIMD then
+// come from different work items with their own barriers: one's MFMAs overlap the other's
+// softmax without any phase arrangement, one item's start (loads) and end (stores) overlap the
+// other's tiles, and no item merges halves at its end. Used when the plan has enough items to
+// give every CU two (kFwdLeanMinItems).
+// --------------------------------------------------------------------------------------------
+namespace fwdl {
+constexpr int NW = fwd::NS;     // waves = query strips
+constexpr int NT = NW * 64;
+constexpr int BN = fwd::BN, D = fwd::D, TILE = fwd::TILE;
+constexpr int STAGE = 2 * TILE;  // K, V of one 64-key tile
+constexpr int BM = fwd::BM;
+static_assert(BM * D <= STAGE, "the Q tile fits in one stage");
+}  // namespace fwdl
+
+template <class E>
+__global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
+    const int4* __restrict__ items, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int hq, int hkv,
+    uint16_t* __restrict__ o, float* __restrict__ lse, int n_tokens, float scale_log2) {
+  using namespace fwdl;
+  __shared__ __attribute__((aligned(16))) uint16_t smem_raw[2 * STAGE];
+  lds_u16* smem = (lds_u16*)smem_raw;
+
+  const int4 it = items[blockIdx.x];
+  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w;
+  if (q0 >= doc_end || doc_start < 0 || q0 < doc_start || doc_end > n_tokens || h < 0 || h >= hq)
+    return;
+  const int group = hq / hkv;
+  const int kvh = h / group;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int strip = wave;
+  const int src = lane & 15, grp = lane >> 4;
+  const long qrow = (long)hq * D, kvrow = (long)hkv * D;
+  const int wq0 = q0 + 32 * strip;
+  const int my_q = wq0 + l32;
+  const bool q_valid = my_q < doc_end;
+  const int ws = __builtin_amdgcn_readfirstlane(strip);
+  const int wq0_u = __builtin_amdgcn_readfirstlane(wq0);
+
+  const int kv_end = min(q0 + BM, doc_end);
+  const int n_tiles = (kv_end - doc_start + BN - 1) / BN;
+
+  // Copy of tile t (K and V) into a stage: wave s moves row groups 4 s .. 4 s + 3 (4 rows each)
+  // of both tensors, 8 instructions; lane i lands in chunk slot i & 15 of row i >> 4 of the group
+  // and fetches logical chunk (i & 15) ^ swz16(row). Rows past the document end read as zeros.
+  int coff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * (4 * strip + j) + (lane >> 4);
+    coff[j] = (r * (int)kvrow + 8 * ((lane & 15) ^ swz16(r))) * 2;
+  }
+  auto copy_tile = [&](int t, int stage) {
+    const int row0 = doc_start + t * BN;
+    const long base = (long)row0 * kvrow + kvh * D;
+    const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
+    const uint32_t dst = lds_addr(smem + stage * STAGE);
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const u32x4 r = make_rsrc4((x ? v : k) + base, bytes);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dma16_opaque(r, dst + (x * TILE + 4 * (4 * ws + j) * D) * 2, coff[j]);
+    }
+  };
+
+  int koff[8], toff[4][2];
+  {
+    const int r = perm32(l32), f = swz16(r);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) koff[kk] = r * D + 8 * ((2 * kk + hi) ^ f);
+    const int sg = (((src & 3) & 1) << 1) | ((src & 3) >> 1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int rr = 8 * hi + 2 * (src >> 2) + e;
+        const int lc = 2 * (grp & 1) + 4 * db + (sg >> 1);
+        toff[db][e] = rr * D + 8 * (lc ^ swz16(rr)) + 4 * (sg & 1);
+      }
+  }
+
+  u32x4 qf[8];
+  f32x16 oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // S^T of one 64-key tile (K at `kb`): 16 MFMAs, each K operand read 4 MFMAs ahead.
+  auto s_tile = [&](const lds_u16* kb, f32x16(&s)[2]) {
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+    u32x4 ka[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ka[i] = ld128(kb + koff[i >> 1] + 32 * (i & 1) * D);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = i >> 1, b = i & 1;
+      s[b] = E::mfma(ka[i & 3], qf[kk], s[b]);
+      if (i + 4 < 16) ka[i & 3] = ld128(kb + koff[(i + 4) >> 1] + 32 * ((i + 4) & 1) * D);
+    }
+    VA_SCHED(kSchedDsRead, 4);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      VA_SCHED(kSchedMfma, 1);
+      VA_SCHED(kSchedDsRead, 1);
+    }
+    VA_SCHED(kSchedMfma, 4);
+  };
+  // Mask, online softmax and O^T += V^T P^T of tile t (V at `vb`), as in the two-half kernel.
+  auto pv_tile = [&](const lds_u16* vb, int t, f32x16(&s)[2]) {
+    const int kv0 = doc_start + t * BN;
+    auto v_read = [&](int i) {
+      const int b = i >> 3, c = (i >> 2) & 1, db = i & 3;
+      const lds_u16* p = vb + (32 * b + 16 * c) * D;
+      const u32x2 x = ldtr(p + toff[db][0]), y = ldtr(p + toff[db][1]);
+      return u32x4{x[0], x[1], y[0], y[1]};
+    };
+    u32x4 va[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = v_read(i);
+    if (kv0 + BN - 1 > wq0_u) {
+      const int lim = my_q - kv0;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (32 * b + reg_row(j, hi) > lim) s[b][j] = -INFINITY;
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mt = fmaxf(mt, s[b][j]);
+    mt = max_with_other_half(mt) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + fwd::kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float rs = 0.f;
+    u32x4 pf[2][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(s[b][8 * c + e], scale_log2, -m_use));
+        pf[b][c] = pack8_tr<E>(p);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) rs = E::sum2(pf[b][c][w], rs);
+      }
+    l_run += rs;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = i >> 3, c = (i >> 2) & 1, db = i & 3;
+      oacc[db] = E::mfma(va[i & 3], pf[b][c], oacc[db]);
+      if (i + 4 < 16) va[i & 3] = v_read(i + 4);
+    }
+  };
+
+  // Q (32 KB) into the second stage, tile 0 into the first; every lane reads its query's row.
+  {
+    const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(h + 1) * D) * 2;
+    const u32x4 rq = make_rsrc4(q + (long)q0 * qrow, bytes);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 32 * strip + 4 * j + (lane >> 4);
+      dma16_opaque(rq, lds_addr(smem + STAGE + (32 * ws + 4 * j) * D),
+                   (r * (int)qrow + h * D + 8 * ((lane & 15) ^ swz16(r))) * 2);
+    }
+  }
+  copy_tile(0, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  {
+    const int r = 32 * strip + l32, f = swz16(r);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + STAGE + r * D + 8 * ((2 * kk + hi) ^ f));
+  }
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
+  __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
+  auto visible = [&](int t) { return doc_start + t * BN <= wq0_u + 31; };
+  for (int t = 0; t < n_tiles; ++t) {
+    const int stage = t & 1;
+    // The next tile's copies go out after this tile's S^T MFMAs (the wave waits for S anyway).
+    if (visible(t)) {
+      f32x16 s[2];
+      s_tile(smem + stage * STAGE, s);
+      if (t + 1 < n_tiles) copy_tile(t + 1, stage ^ 1);
+      pv_tile(smem + stage * STAGE + TILE, t, s);
+    } else if (t + 1 < n_tiles) {
+      copy_tile(t + 1, stage ^ 1);
+    }
+    wait_vmcnt<0>();  // this wave's copies of the next tile have landed in LDS
+    __syncthreads();
+  }
+
+  // O = O^T / l per query, written as whole 256-byte rows through this wave's own LDS row tile
+  // (the stages are free after the last barrier); lse = (m + log2 l) ln 2.
+  const float l_tot = sum_with_other_half(l_run);
+  const float inv = 1.f / l_tot;
+  u32x4 w[8];  // chunk 2 db + c: d = 32 db + 16 c + 8 hi + 0..7 of query wq0 + l32
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      w[2 * db + c] = pack8<E>(oacc[db][8 * c] * inv, oacc[db][8 * c + 1] * inv,
+                               oacc[db][8 * c + 2] * inv, oacc[db][8 * c + 3] * inv,
+                               oacc[db][8 * c + 4] * inv, oacc[db][8 * c + 5] * inv,
+                               oacc[db][8 * c + 6] * inv, oacc[db][8 * c + 7] * inv);
+  static_assert(NW * 32 * (8 * 16 + 8) * 2 <= 2 * STAGE * 2, "row tiles fit in LDS");
+  store_rows32<16>(smem + strip * 32 * (8 * 16 + 8), w, lane,
+                   [&](int r) { return o + (long)(wq0 + r) * qrow + h * D; }, doc_end - wq0);
+  if (q_valid && hi == 0) {
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    __builtin_nontemporal_store((m_use + fast_log2(l_tot)) * kLn2, &lse[(long)h * n_tokens + my_q]);
+  }
+}
+
 template <class E>
 static hipError_t launch_fwd_t(const FwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
+  if (a.n_items >= kFwdLeanMinItems) {
+    hipLaunchKernelGGL((fwd_lean_kernel<E>), dim3((unsigned)a.n_items), dim3(fwdl::NT), 0,
+                       a.stream, (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
+                       (const uint16_t*)a.v, a.hq, a.hkv, (uint16_t*)a.out, a.lse,
+                       (int)a.n_tokens, a.scale * kLog2e);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((fwd_kernel<E>), dim3((unsigned)a.n_items), dim3(fwd::NT), 0, a.stream,
                      (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, a.hq, a.hkv, (uint16_t*)a.out, a.lse, (int)a.n_tokens,

@@ -89,6 +89,41 @@ def test_varlen_matches_oracle(lengths, hq, hkv, dtype):
     check_all(out, grads, oracle(q, k, v, do, lengths), dtype, sum(lengths), hq)
 
 
+def padded_fwd_plan(plan, min_items):
+    """The forward items of `plan` followed by empty items up to `min_items`: a list that long
+    runs the many-item (4-wave, two work-groups per CU) forward kernel on the same real items."""
+    items = torch.zeros(max(min_items, plan.n_fwd), 4, dtype=torch.int32, device="cuda")
+    items[: plan.n_fwd] = plan.fwd_items[: plan.n_fwd]
+    return items
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
+def test_many_item_forward_matches_oracle(lengths, hq, hkv, dtype):
+    """The forward kernel that runs for plans of many items (>= kFwdLeanMinItems = 512; one wave
+    per query strip over all key tiles, no halves to merge), forced on small cases by padding the
+    plan with empty items: O and lse against the oracle, and the backward run from them."""
+    qk = 3.0 if dtype == "peaky" else 1.0
+    dtype = torch.bfloat16 if dtype == "peaky" else dtype
+    banner("many-item forward", lengths, hq, hkv, dtype, qk)
+    q, k, v, do = wl.make_inputs(lengths, hq, hkv, dtype, seed=sum(lengths) + 1, qk_scale=qk)
+    n = sum(lengths)
+    dev = torch.device("cuda")
+    plan = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
+    items = padded_fwd_plan(plan, 512)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    out = torch.empty_like(qd)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+    att.check(att.lib().va_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                               lse.data_ptr(), items.data_ptr(), items.shape[0], n, hq, hkv, 128,
+                               SCALE, 0 if dtype == torch.float16 else 1, att._stream()), "va_fwd")
+    dq, dk, dv = att.attention_backward(do.to(dev), qd, kd, vd, out, lse, plan, SCALE)
+    torch.cuda.synchronize()
+    ref = oracle(q, k, v, do, lengths)
+    err_lse = float(np.max(np.abs(lse.cpu().numpy() - ref[1])))
+    assert err_lse <= TOL[dtype]["lse"], err_lse
+    check_all(out.cpu(), (dq.cpu(), dk.cpu(), dv.cpu()), ref, dtype, n, hq)
+
+
 @pytest.mark.parametrize("name", sorted(GOLDEN))
 def test_golden_vectors(name):
     z = load_golden(name)
@@ -613,3 +648,15 @@ def test_kernels_skip_items_of_a_plan_for_other_sizes():
     # the first two documents are the same in both plans: their rows are right
     ref = oracle(q.cpu(), k.cpu(), v.cpu(), do.cpu(), small)
     check_all(out.cpu(), (dq.cpu(), dk.cpu(), dv.cpu()), ref, torch.float16, n, hq_small)
+    # the many-item forward kernel (the same list padded with empty items) skips the same items
+    items = padded_fwd_plan(plan_big, 512)
+    ob2, out2 = canaried((n, hq_small, 128), torch.float16)
+    lb2, lse2 = canaried((hq_small, n), torch.float32)
+    att.check(lib.va_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out2.data_ptr(),
+                         lse2.data_ptr(), items.data_ptr(), items.shape[0], n, hq_small, hkv, 128,
+                         SCALE, 0, att._stream()), "va_fwd")
+    torch.cuda.synchronize()
+    for buf in (ob2, lb2):
+        assert torch.isnan(buf[:pad].float()).all() and torch.isnan(buf[-pad:].float()).all()
+    err_o = float(np.max(np.abs(out2.cpu().float().numpy() - ref[0])))
+    assert err_o <= TOL[torch.float16]["o"], err_o
