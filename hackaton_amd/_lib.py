@@ -14,6 +14,7 @@ VA_F16, VA_BF16, VA_F32 = 0, 1, 2
 VA_PLAN_FWD, VA_PLAN_BWD = 0, 1
 VA_LAYOUT_PACKED, VA_LAYOUT_PADDED = 0, 1
 VA_BWD_MAIN, VA_BWD_FINISH = 1, 2
+VA_FWD_MANY_ITEMS = 512
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -9,6 +9,8 @@
 #include "va_api_internal.h"
 #include "va_kernels.h"
 
+static_assert(va::kFwdLeanMinItems == VA_FWD_MANY_ITEMS, "forward kernel switch: header and kernels");
+
 namespace va {
 
 char* last_error_buffer() {

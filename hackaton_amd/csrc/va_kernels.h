@@ -11,8 +11,8 @@ constexpr int kHeadDim = 128;  // Qwen2.5-1.5B / 7B head size; the kernels are b
 // Tile geometry; the plan builder (plan.cpp) emits work items for exactly these shapes.
 constexpr int kFwdWaves = 4;                 // forward: 32 queries per wave
 constexpr int kFwdBlockM = 32 * kFwdWaves;   // queries per forward work item
-// From this many forward items on, the 4-wave forward (two work-groups per CU) runs instead of
-// the 8-wave one: every CU then gets at least two items.
+// From this many forward items on (VA_FWD_MANY_ITEMS), the 4-wave forward (two work-groups per
+// CU) runs instead of the 8-wave one: every CU then gets at least two items.
 constexpr int kFwdLeanMinItems = 512;
 constexpr int kBwdBlockN = 128;  // keys per backward kv work item
 constexpr int kBwdBlockQ = 32;   // queries per kv-item step

@@ -108,7 +108,11 @@ int va_stream_capture_id(void* stream, uint64_t* capture_id);
 /* ---- attention forward ------------------------------------------------------------------------
  * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row;
  * scale must be finite and > 0 (D^-0.5 in the reference).
+ * From VA_FWD_MANY_ITEMS items on (n_items, empty items included) va_fwd runs its many-item
+ * kernel (4 waves per item, two work-groups per CU) instead of the 8-wave one; both compute the
+ * same function (results agree to rounding, each is deterministic).
  * Replaces: solution/attention.py:221-222 (aten::_efficient_attention_forward). */
+enum { VA_FWD_MANY_ITEMS = 512 };
 int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
            const int32_t* items, int64_t n_items, int64_t total_tokens, int32_t hq, int32_t hkv,
            int32_t head_dim, float scale, int32_t dtype, void* stream);

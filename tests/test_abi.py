@@ -219,3 +219,19 @@ def test_device_plan_rejects_bad_arguments_before_launching():
                                     None) == _lib.VA_ECAPACITY
     assert lib.va_plan_build_device(fake, 1, 100, 12, 5, _lib.VA_PLAN_FWD, fake, 1000,
                                     None) == _lib.VA_ESHAPE
+
+
+def test_header_constants_match_python():
+    """Every enum constant of include/varlen_attn.h has the same value in hackaton_amd._lib."""
+    import re
+    from pathlib import Path
+
+    text = (Path(__file__).resolve().parent.parent / "include" / "varlen_attn.h").read_text()
+    consts = {}
+    for body in re.findall(r"enum\s*\{([^}]*)\}", text):
+        for name, value in re.findall(r"(VA_\w+)\s*=\s*(-?\d+)", body):
+            consts[name] = int(value)
+    assert "VA_FWD_MANY_ITEMS" in consts and "VA_PLAN_BWD" in consts
+    for name, value in consts.items():
+        if hasattr(_lib, name):
+            assert getattr(_lib, name) == value, name
