@@ -10,6 +10,9 @@
 #include "va_kernels.h"
 
 static_assert(va::kFwdLeanMinItems == VA_FWD_MANY_ITEMS, "forward kernel switch: header and kernels");
+static_assert(va::kBwdPairMinItems == VA_BWD_PAIR_MIN_ITEMS && VA_PLAN_BWD_HEADS == 2 &&
+                  VA_PLAN_BWD_PAIRS == 3,
+              "backward plan kinds: header and planners");
 
 namespace va {
 

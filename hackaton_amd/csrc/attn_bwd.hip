@@ -46,10 +46,13 @@ constexpr int Q_HALFS = 2 * Q_PAIR;
 constexpr int HALFS = KV_HALFS > Q_HALFS ? KV_HALFS : Q_HALFS;
 static_assert(BK == kBwdBlockN && QB == kBwdBlockM && BQ == kBwdBlockQ, "plan tile sizes");
 constexpr int kKindKV = 0, kKindQ = 1;
+constexpr int kHeadMask = (1 << 20) - 1;  // item word: kind << 24 | pair << 20 | head
 }  // namespace bwd
 
 // --------------------------------------------------------------------------------------------
-// kv item: dK, dV of 128 keys for one query head.
+// kv item: dK, dV of 128 keys for one query head, or (pair items) for two query heads h, h + 1
+// of one GQA group: then half j takes head h + j over every query step, so the halves share the
+// K/V tile, never exchange accumulators, and each writes both partials of its head.
 // --------------------------------------------------------------------------------------------
 template <class E>
 __device__ __forceinline__ void bwd_kv_item(
@@ -60,7 +63,8 @@ __device__ __forceinline__ void bwd_kv_item(
     uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part, int n_tokens, int hq,
     int hkv, float scale, float scale_log2) {
   using namespace bwd;
-  const int k0 = it.x, doc_end = it.y, h = it.w & 0xffffff;
+  const int k0 = it.x, doc_end = it.y, h = it.w & kHeadMask;
+  const bool pair = (it.w >> 20) & 1;
   const int kvh = h / (hq / hkv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
   const int half = wave / NS, strip = wave % NS;
@@ -81,7 +85,11 @@ __device__ __forceinline__ void bwd_kv_item(
   }
 
   const int n_steps = (doc_end - k0 + BQ - 1) / BQ;
-  const int n_pairs = (n_steps + 1) / 2;
+  // Iterations of the step loop: a step pair of one head (the halves take alternate steps), or
+  // one step of each head of a pair item.
+  const int n_iter = pair ? n_steps : (n_steps + 1) / 2;
+  auto step_of = [&](int p, int j) { return pair ? p : 2 * p + j; };  // step of half j at p
+  auto head_of = [&](int j) { return pair ? h + j : h; };
 
   // Staging of a step pair: thread chunk i is (step half i >> 1, tensor i & 1 = Q / dO), row
   // tid >> 4, 16-byte column tid & 15, through buffer loads bounded at the document end (rows past
@@ -89,23 +97,26 @@ __device__ __forceinline__ void bwd_kv_item(
   // until the store, where its dot product with the dO chunk gives delta = rowsum(dO * O): the
   // loads are then complete and the dot product does not stall the step.
   const int s_row = tid >> 4, s_col = 8 * (tid & 15);
-  const int s_voff = (s_row * (int)qrow + h * D + s_col) * 2;
+  const int s_voff = (s_row * (int)qrow + s_col) * 2;  // + the head's column, per step half
   u32x4 sreg[4], oreg[2];
   float st_lse = 0.f;
   int st_row = 0;
   auto gload_pair = [&](int p) {
 #pragma unroll
     for (int sh = 0; sh < 2; ++sh) {
-      const int qs0 = k0 + min(2 * p + sh, n_steps - 1) * BQ;
+      const int hs = head_of(sh);
+      const int qs0 = k0 + min(step_of(p, sh), n_steps - 1) * BQ;
       const long base = (long)qs0 * qrow;
-      const long bytes = ((long)(doc_end - qs0 - 1) * qrow + (long)(h + 1) * D) * 2;
-      sreg[2 * sh] = bload16(make_rsrc(q + base, bytes), s_voff);
-      sreg[2 * sh + 1] = bload16(make_rsrc(dout + base, bytes), s_voff);
-      oreg[sh] = bload16(make_rsrc(out + base, bytes), s_voff);
+      const long bytes = ((long)(doc_end - qs0 - 1) * qrow + (long)(hs + 1) * D) * 2;
+      const int voff = s_voff + hs * D * 2;
+      sreg[2 * sh] = bload16(make_rsrc(q + base, bytes), voff);
+      sreg[2 * sh + 1] = bload16(make_rsrc(dout + base, bytes), voff);
+      oreg[sh] = bload16(make_rsrc(out + base, bytes), voff);
     }
     if (tid < 64) {  // raw value: scaled at the store, so that no wait follows the loads here
-      st_row = k0 + min(2 * p + (tid >> 5), n_steps - 1) * BQ + (tid & 31);
-      st_lse = lse[(long)h * n_tokens + min(st_row, doc_end - 1)];
+      const int sh = tid >> 5;
+      st_row = k0 + min(step_of(p, sh), n_steps - 1) * BQ + (tid & 31);
+      st_lse = lse[(long)head_of(sh) * n_tokens + min(st_row, doc_end - 1)];
     }
   };
   auto store_pair = [&](int stage) {
@@ -148,10 +159,10 @@ __device__ __forceinline__ void bwd_kv_item(
   }
   store_pair(0);
   __syncthreads();
-  for (int p = 0; p < n_pairs; ++p) {
+  for (int p = 0; p < n_iter; ++p) {
     const int stage = p & 1;
-    if (p + 1 < n_pairs) gload_pair(p + 1);
-    const int s = 2 * p + half;
+    if (p + 1 < n_iter) gload_pair(p + 1);
+    const int s = step_of(p, half);
     const int qs0 = k0 + s * BQ;
     if (s < n_steps && kw0 <= qs0 + BQ - 1) {
       const lds_u16* qs = smem + KV_OFF_Q + (stage * 2 + half) * ROWT;
@@ -241,7 +252,7 @@ __device__ __forceinline__ void bwd_kv_item(
         __builtin_amdgcn_sched_barrier(0);  // keep the reads 3 MFMAs ahead: not sunk to their use
       }
     }
-    if (p + 1 < n_pairs) store_pair(stage ^ 1);
+    if (p + 1 < n_iter) store_pair(stage ^ 1);
     __syncthreads();
   }
 
@@ -282,6 +293,39 @@ __device__ __forceinline__ void bwd_kv_item(
     store_rows32<16>(reinterpret_cast<lds_u16*>(&xs[slot(half, 0, 0) - lane]), w, lane,
                     [&](int r) { return part + ((long)(kw0 + r) * hq + h) * D; }, doc_end - kw0);
   };
+  if (pair) {
+    // Each half holds the whole dK/dV of its head: both go out through this wave's own row tile
+    // (the LDS stages are free after the loop's last barrier), dK scaled.
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar: no VGPR kept
+    const int head_w = pair ? h + (wv >> 2) : h;                         // across the loop
+    lds_u16* tile = smem + wv * 32 * (8 * 8 + 8);
+    static_assert(NW * 32 * (8 * 8 + 8) <= HALFS, "per-wave row tiles fit in LDS");
+    // 64 columns at a time (db 2 c2, 2 c2 + 1), so that few registers are live beside the
+    // accumulators.
+    auto store = [&](const f32x16(&acc)[4], float mul, uint16_t* part) {
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        u32x4 w[4];
+#pragma unroll
+        for (int db2 = 0; db2 < 2; ++db2)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const f32x16& a = acc[2 * c2 + db2];
+            w[2 * db2 + c] = pack8<E>(a[8 * c] * mul, a[8 * c + 1] * mul, a[8 * c + 2] * mul,
+                                      a[8 * c + 3] * mul, a[8 * c + 4] * mul, a[8 * c + 5] * mul,
+                                      a[8 * c + 6] * mul, a[8 * c + 7] * mul);
+          }
+        store_rows32<8>(tile, w, lane,
+                        [&](int r) {
+                          return part + ((long)(kw0 + r) * hq + head_w) * D + 64 * c2;
+                        },
+                        doc_end - kw0);
+      }
+    };
+    store(dkacc, scale, dk_part);
+    store(dvacc, 1.f, dv_part);
+    return;
+  }
   if (half) finish(dvacc, dkacc, 1.f, dv_part);
   else finish(dkacc, dvacc, scale, dk_part);
 }
@@ -297,7 +341,7 @@ __device__ __forceinline__ void bwd_q_item(
     const float* __restrict__ lse, uint16_t* __restrict__ dq, int n_tokens, int hq, int hkv,
     float scale, float scale_log2, float* stat_f) {
   using namespace bwd;
-  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & 0xffffff;
+  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kHeadMask;
   const int kvh = h / (hq / hkv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
   const int half = wave / NS, strip = wave % NS;
@@ -504,9 +548,11 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
   const int4 it = items[blockIdx.x];
   // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
   // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
-  const int kind = it.w >> 24, h = it.w & 0xffffff;
+  const int kind = it.w >> 24, h = it.w & bwd::kHeadMask, pair = (it.w >> 20) & 15;
+  // Pair items (kv only) take heads h, h + 1 of one GQA group.
   if (it.x >= it.y || it.z < 0 || it.x < it.z || it.y > n_tokens || h >= hq ||
-      (kind != bwd::kKindKV && kind != bwd::kKindQ))
+      (kind != bwd::kKindKV && kind != bwd::kKindQ) || pair > 1 ||
+      (pair && (kind != bwd::kKindKV || h + 1 >= hq || h / (hq / hkv) != (h + 1) / (hq / hkv))))
     return;
   if (kind == bwd::kKindKV) {
     bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,

@@ -43,8 +43,17 @@ int check_heads(int32_t hq, int32_t hkv) {
 constexpr int64_t kKvItemCost = va::kPlanKvItemCost;
 constexpr int64_t kQItemCost = va::kPlanQItemCost;
 
-std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
+bool is_plan_kind(int32_t kind) {
+  return kind == VA_PLAN_FWD || kind == VA_PLAN_BWD || kind == VA_PLAN_BWD_HEADS ||
+         kind == VA_PLAN_BWD_PAIRS;
+}
+int32_t item_head(int32_t d) { return d & (va::kItemPairBit - 1); }
+
+std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv,
+                             int32_t kind) {
   std::vector<Item> items;
+  const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
+  const int32_t group = hq / hkv, rows = pairs ? (group + 1) / 2 : group;
   for (int32_t i = 0; i < n_docs; ++i) {
     const int32_t s = cu[i], e = cu[i + 1];
     if (e <= s) continue;
@@ -62,10 +71,16 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
       // tile pair + ~2.4 us per q item; hence 39 and 30. Without the fixed cost a kv item over
       // 384 queries (18.7 us) ties with a q item over 512 keys (17.3 us), and the XCD layout
       // below deals the heavier ones to the same XCDs in every block.
+      // A pair item's halves each take one head over every step: twice a per-head item's steps.
       for (int32_t k0 = s; k0 < e; k0 += va::kBwdBlockN) {
         const int64_t steps = ((int64_t)e - k0 + va::kBwdBlockQ - 1) / va::kBwdBlockQ;
-        const int64_t work = (steps + 1) / 2 * 32 + kKvItemCost;
-        for (int32_t h = 0; h < hq; ++h) items.push_back({k0, e, s, h, work});
+        for (int32_t g = 0; g < hkv; ++g)
+          for (int32_t r = 0; r < rows; ++r) {
+            const bool pair = pairs && 2 * r + 1 < group;
+            const int32_t h = g * group + (pairs ? 2 * r : r);
+            const int64_t work = (pair ? steps : (steps + 1) / 2) * 32 + kKvItemCost;
+            items.push_back({k0, e, s, (pair ? va::kItemPairBit : 0) | h, work});
+          }
       }
       for (int32_t q0 = s; q0 < e; q0 += va::kBwdBlockM) {
         const int64_t kv_end = std::min<int64_t>((int64_t)q0 + va::kBwdBlockM, e);
@@ -91,10 +106,10 @@ std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
   std::vector<std::vector<Item>> combos;
   for (const Item& x : v) {
     const Item* last = combos.empty() ? nullptr : &combos.back().front();
-    const int32_t h = x.d & 0xffffff, kind = x.d >> 24;
+    const int32_t h = item_head(x.d), kind = x.d >> 24;
     if (last != nullptr && (int32_t)combos.back().size() < group && last->a == x.a &&
         last->b == x.b && last->c == x.c && (last->d >> 24) == kind &&
-        (last->d & 0xffffff) / group == h / group) {
+        item_head(last->d) / group == h / group) {
       combos.back().push_back(x);
     } else {
       combos.push_back({x});
@@ -102,24 +117,30 @@ std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
   }
   std::vector<Item> out;
   out.reserve(v.size());
-  for (size_t c0 = 0; c0 < combos.size(); c0 += kXcds) {
-    const size_t c1 = std::min(combos.size(), c0 + kXcds);
-    for (int32_t r = 0; r < group; ++r)
-      for (size_t c = c0; c < c1; ++c)
-        if (r < (int32_t)combos[c].size()) out.push_back(combos[c][r]);
+  // A block takes up to 8 consecutive combos of one size (pair plans mix kv combos of G / 2
+  // items with q combos of G), so that every combo's items sit one stride apart.
+  for (size_t c0 = 0; c0 < combos.size();) {
+    size_t c1 = c0 + 1;
+    while (c1 < combos.size() && c1 - c0 < (size_t)kXcds && combos[c1].size() == combos[c0].size())
+      ++c1;
+    for (size_t r = 0; r < combos[c0].size(); ++r)
+      for (size_t c = c0; c < c1; ++c) out.push_back(combos[c][r]);
+    c0 = c1;
   }
   return out;
 }
 
-int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
+int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind) {
   int64_t n = 0;
+  const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
+  const int64_t kv_per_tile = pairs ? (int64_t)hkv * ((hq / hkv + 1) / 2) : hq;
   for (int32_t i = 0; i < n_docs; ++i) {
     const int64_t len = (int64_t)cu[i + 1] - cu[i];
     if (len <= 0) continue;
     if (kind == VA_PLAN_FWD) {
       n += (len + va::kFwdBlockM - 1) / va::kFwdBlockM * hq;
     } else {
-      n += (len + va::kBwdBlockN - 1) / va::kBwdBlockN * hq;
+      n += (len + va::kBwdBlockN - 1) / va::kBwdBlockN * kv_per_tile;
       n += (len + va::kBwdBlockM - 1) / va::kBwdBlockM * hq;
     }
   }
@@ -131,12 +152,12 @@ int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind)
 extern "C" int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv,
                             int32_t kind, int64_t* n_items) {
   if (n_items == nullptr) return va::fail(VA_EINVAL, "n_items is NULL");
-  if (kind != VA_PLAN_FWD && kind != VA_PLAN_BWD) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
+  if (!is_plan_kind(kind)) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
   int rc = check_heads(hq, hkv);
   if (rc) return rc;
   rc = check_cu(cu_seqlens, n_docs);
   if (rc) return rc;
-  *n_items = count_items(cu_seqlens, n_docs, hq, kind);
+  *n_items = count_items(cu_seqlens, n_docs, hq, hkv, kind);
   return VA_OK;
 }
 
@@ -149,7 +170,7 @@ extern "C" int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t 
   if (n > capacity) return va::fail(VA_ECAPACITY, "plan needs %lld items, capacity %lld",
                                     (long long)n, (long long)capacity);
   if (n > 0 && items == nullptr) return va::fail(VA_EINVAL, "items is NULL");
-  const std::vector<Item> v = xcd_order(make_items(cu_seqlens, n_docs, hq, kind), hq / hkv);
+  const std::vector<Item> v = xcd_order(make_items(cu_seqlens, n_docs, hq, hkv, kind), hq / hkv);
   for (size_t i = 0; i < v.size(); ++i) {
     items[4 * i + 0] = v[i].a;
     items[4 * i + 1] = v[i].b;
@@ -162,7 +183,7 @@ extern "C" int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t 
 extern "C" int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t kind,
                                 int64_t* capacity) {
   if (capacity == nullptr) return va::fail(VA_EINVAL, "capacity is NULL");
-  if (kind != VA_PLAN_FWD && kind != VA_PLAN_BWD) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
+  if (!is_plan_kind(kind)) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
   if (n_tokens < 0 || n_tokens > INT32_MAX / 2)
     return va::fail(VA_ESHAPE, "n_tokens=%lld out of range", (long long)n_tokens);
   if (n_docs < 0 || n_docs > va::kPlanMaxDocs)
@@ -195,13 +216,14 @@ extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_
                                     int32_t* items_device, int64_t capacity, void* stream) {
   int rc = check_heads(hq, hkv);
   if (rc) return rc;
-  if (kind != VA_PLAN_FWD && kind != VA_PLAN_BWD) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
+  if (!is_plan_kind(kind)) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
   if (cu_seqlens_device == nullptr) return va::fail(VA_EINVAL, "cu_seqlens_device is NULL");
   if ((rc = check_device_plan(n_tokens, n_docs, hq, hkv, kind, items_device, capacity))) return rc;
   const bool fwd = kind == VA_PLAN_FWD;
   const hipError_t e = va::launch_plan_device(
       cu_seqlens_device, nullptr, n_docs, (int)n_tokens, hq, hkv, fwd ? items_device : nullptr,
-      capacity, fwd ? nullptr : items_device, capacity, nullptr, (hipStream_t)stream);
+      capacity, fwd ? nullptr : items_device, capacity,
+      !fwd && va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, kind), nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return va::fail((int)e, "va_plan_build_device launch: %s", hipGetErrorString(e));
   return VA_OK;
 }
@@ -224,10 +246,10 @@ extern "C" int va_plan_build_device_lengths(const int64_t* lengths_device, int32
       (rc = check_device_plan(n_tokens, n_docs, hq, hkv, VA_PLAN_BWD, bwd_items_device,
                               bwd_capacity)))
     return rc;
-  const hipError_t e = va::launch_plan_device(nullptr, lengths_device, n_docs, (int)n_tokens, hq,
-                                              hkv, fwd_items_device, fwd_capacity,
-                                              bwd_items_device, bwd_capacity, cu_seqlens_out,
-                                              (hipStream_t)stream);
+  const hipError_t e = va::launch_plan_device(
+      nullptr, lengths_device, n_docs, (int)n_tokens, hq, hkv, fwd_items_device, fwd_capacity,
+      bwd_items_device, bwd_capacity, va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, VA_PLAN_BWD),
+      cu_seqlens_out, (hipStream_t)stream);
   if (e != hipSuccess)
     return va::fail((int)e, "va_plan_build_device_lengths launch: %s", hipGetErrorString(e));
   return VA_OK;

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
                                                   int n_tokens, int hq, int hkv,
                                                   int4* __restrict__ fwd_items, long fwd_capacity,
                                                   int4* __restrict__ bwd_items, long bwd_capacity,
-                                                  int32_t* __restrict__ cu_out) {
+                                                  int bwd_pairs, int32_t* __restrict__ cu_out) {
   __shared__ int s_bound[kPlanMaxDocs + 1];  // clamped, non-decreasing document bounds
   __shared__ int s_tbase[kPlanMaxDocs + 1];  // exclusive prefix of the per-document tile counts
   __shared__ int s_cnt[kBuckets];
@@ -77,6 +77,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   const long capacity = kind == VA_PLAN_FWD ? fwd_capacity : bwd_capacity;
   if (items == nullptr) return;  // uniform over the work-group
   const int group = hq / hkv;
+  const bool pairs = kind == VA_PLAN_BWD && bwd_pairs;  // kv items of two heads each
 
   // Document bounds, DPB per thread.
   if (lengths != nullptr) {
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       work = min(s + (long)(t + 1) * kTile, e) - s;
     } else if (!is_q) {
       const long steps = (e - (s + (long)t * kTile) + kBwdBlockQ - 1) / kBwdBlockQ;
-      work = (steps + 1) / 2 * 32 + kPlanKvItemCost;
+      work = (pairs ? steps : (steps + 1) / 2) * 32 + kPlanKvItemCost;
     } else {
       const long kv_end = min(s + (long)(t + 1) * kTile, e);
       const long tiles = (kv_end - s + kBwdTileK - 1) / kBwdTileK;
@@ -210,7 +211,9 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   __syncthreads();
   // Candidate at sorted position `pos` holds combos pos * Hkv + g (g = GQA group); combo j sits
   // in column j % 8 of block j / 8, which spans 8 G slots (fewer columns in the last block);
-  // head r of the group goes to row r.
+  // head r of the group goes to row r. In a pair plan a kv combo's row r < ceil(G / 2) holds the
+  // item of heads 2 r, 2 r + 1 (the last head of an odd group alone) and its other rows stay
+  // empty items.
   const long n_combos = (long)n_cand * hkv;
   for (int c = tid; c < n_cand; c += PT) {
     int doc, t, is_q;
@@ -223,7 +226,14 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       const long ncols = min((long)kXcds, n_combos - blk * kXcds);
       for (int r = 0; r < group; ++r) {
         const long slot = blk * kXcds * group + r * ncols + col;
-        if (slot < capacity) items[slot] = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
+        int4 item = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
+        if (pairs && !is_q) {
+          const int h2 = 2 * r;
+          item = h2 < group ? int4{s + t * kTile, e, s,
+                                   (h2 + 1 < group ? kItemPairBit : 0) | (g * group + h2)}
+                            : int4{0, 0, 0, 0};
+        }
+        if (slot < capacity) items[slot] = item;
       }
     }
   }
@@ -234,10 +244,11 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
 
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
-                              int32_t* bwd_items, long bwd_capacity, int32_t* cu_out,
-                              hipStream_t stream) {
+                              int32_t* bwd_items, long bwd_capacity, bool bwd_pairs,
+                              int32_t* cu_out, hipStream_t stream) {
   hipLaunchKernelGGL(plan_kernel, dim3(2), dim3(PT), 0, stream, cu, lengths, n_docs, n_tokens, hq,
-                     hkv, (int4*)fwd_items, fwd_capacity, (int4*)bwd_items, bwd_capacity, cu_out);
+                     hkv, (int4*)fwd_items, fwd_capacity, (int4*)bwd_items, bwd_capacity,
+                     (int)bwd_pairs, cu_out);
   return hipGetLastError();
 }
 

@@ -23,6 +23,16 @@ constexpr int kPlanMaxDocs = 8192;  // documents a device-built plan takes (LDS-
 // wave per step pair: 32 per kv step pair, 24 per q tile pair (from in-graph item durations).
 constexpr int kPlanKvItemCost = 39;
 constexpr int kPlanQItemCost = 30;
+// VA_PLAN_BWD takes two query heads per kv item (pair items, Hq > Hkv) once the per-head list
+// would be this long (2 (ceil(N / 128) + n_docs) Hq items: every CU then holds several).
+constexpr int kBwdPairMinItems = 1024;
+constexpr int kItemPairBit = 1 << 20;  // item word: kind << 24 | pair << 20 | head
+// Whether a backward plan of `kind` for these host-known sizes has pair items.
+inline bool bwd_plan_pairs(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t hkv, int kind) {
+  if (kind == 2 || hkv <= 0 || hq / hkv < 2) return false;  // VA_PLAN_BWD_HEADS, or no group
+  if (kind == 3) return true;                                  // VA_PLAN_BWD_PAIRS
+  return 2 * ((n_tokens + 127) / 128 + n_docs) * (int64_t)hq >= kBwdPairMinItems;
+}
 
 struct FwdArgs {
   const void* q;
@@ -98,7 +108,7 @@ hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, co
 // ones after; cu_out (nullable) receives the clamped document bounds.
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
-                              int32_t* bwd_items, long bwd_capacity, int32_t* cu_out,
-                              hipStream_t stream);
+                              int32_t* bwd_items, long bwd_capacity, bool bwd_pairs,
+                              int32_t* cu_out, hipStream_t stream);
 
 }  // namespace va

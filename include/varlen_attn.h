@@ -51,7 +51,8 @@ enum {
 };
 
 enum { VA_F16 = 0, VA_BF16 = 1, VA_F32 = 2 };
-enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1 };
+enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1, VA_PLAN_BWD_HEADS = 2, VA_PLAN_BWD_PAIRS = 3 };
+enum { VA_BWD_PAIR_MIN_ITEMS = 1024 };
 enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
 enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2 };
 
@@ -61,11 +62,15 @@ int32_t va_head_dim(void);
 
 /* ---- work plan (host only; no GPU call) ------------------------------------------------------
  * Work items for the forward (kind VA_PLAN_FWD: one per 128-query tile x query head) or the
- * backward (VA_PLAN_BWD: one per 128-key tile x query head for dK/dV and one per 128-query tile
- * x query head for dQ) over the documents of cu_seqlens, longest first. The G = Hq / Hkv items of
- * one tile and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the
- * heads sharing K/V run on one XCD and share its L2. Fully masked causal tiles and
- * cross-document tiles never appear.
+ * backward (one per 128-query tile x query head for dQ, and for dK/dV one per 128-key tile x
+ * query head (VA_PLAN_BWD_HEADS) or one per 128-key tile x pair of query heads of one GQA group,
+ * the last head of an odd group alone (VA_PLAN_BWD_PAIRS); VA_PLAN_BWD takes pairs when Hq > Hkv
+ * and the per-head list would hold 2 (ceil(n_tokens / 128) + n_docs) Hq >= VA_BWD_PAIR_MIN_ITEMS
+ * items, heads otherwise) over the documents of cu_seqlens, longest first. The items of one tile
+ * and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the heads
+ * sharing K/V run on one XCD and share its L2. Fully masked causal tiles and cross-document tiles
+ * never appear. Every plan kind gives the same outputs up to rounding (a pair item sums a head's
+ * query steps in one sequence instead of two halves); each is deterministic.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
 int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                  int64_t* n_items);
@@ -77,7 +82,8 @@ int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t
  * by one kernel on `stream`, with no host read (the reference reads the lengths back with
  * lengths.tolist(), solution/packed.py:170-172, before _cu_seqlens at attention.py:195-209).
  * va_plan_capacity gives, from host-known sizes only, the number of items such a plan has:
- * ceil(n_tokens / 128) + n_docs tiles per query head, twice that for VA_PLAN_BWD.
+ * ceil(n_tokens / 128) + n_docs tiles per query head, twice that for the backward kinds (a pair
+ * plan leaves the slots of its missing kv rows empty).
  * va_plan_build_device writes exactly `capacity` items (int32 x 4) to device memory: the real
  * ones longest first, then empty items that va_fwd / va_bwd skip, so the kernels take n_items =
  * capacity. Document bounds are clamped into [0, n_tokens] and made non-decreasing on the device,

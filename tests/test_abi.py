@@ -54,22 +54,26 @@ def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
     check_xcd_order(items, hq, hkv, lambda q0, e, s, w: min(q0 + 128, e) - s)
 
 
-def check_xcd_order(items, hq, hkv, work_of):
-    """The G = Hq / Hkv items of one (tile, kind, GQA group) sit a constant stride apart, at most
-    8 (the XCD count: work-group i runs on XCD i mod 8, so they share one L2), and the groups
-    come longest first."""
+HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | pair << 20 | head
+
+
+def check_xcd_order(items, hq, hkv, work_of, per_combo=None):
+    """The items of one (tile, kind, GQA group, work) sit a constant stride apart, at most 8 (the
+    XCD count: work-group i runs on XCD i mod 8, so they share one L2), `per_combo` of them
+    (default G = Hq / Hkv: one per head), and the groups come longest first."""
     g = hq // hkv
     combos = {}
     for pos, (a, e, s, w) in enumerate(items.tolist()):
-        key = (a, e, s, w >> 24, (w & 0xFFFFFF) // g)
-        combos.setdefault(key, []).append((pos, work_of(a, e, s, w)))
+        work = work_of(a, e, s, w)
+        key = (a, e, s, w >> 24, (w & HEAD_MASK) // g, work)
+        combos.setdefault(key, []).append((pos, work))
     firsts = []
     for key, entries in combos.items():
-        assert len(entries) == g
+        expect = g if per_combo is None else per_combo(key)
+        assert len(entries) == expect, (key, len(entries), expect)
         pos = [p for p, _ in entries]
         steps = {b - a for a, b in zip(pos, pos[1:])}
         assert len(steps) <= 1 and all(0 < x <= 8 for x in steps), (key, pos)
-        assert len({w for _, w in entries}) == 1
         firsts.append((pos[0], entries[0][1]))
     work = [w for _, w in sorted(firsts)]
     assert work == sorted(work, reverse=True)
@@ -90,29 +94,79 @@ def test_backward_plan_deals_every_xcd_the_same_items():
     assert all(m == mixes[0] for m in mixes)
 
 
+def bwd_work(a, e, s, w):
+    """The planners' measure: MFMAs per wave per iteration + item cost (a pair item's halves each
+    take every step of one head; a per-head item's halves take alternate steps)."""
+    if w >> 24 == 0:
+        steps = (e - a + 31) // 32
+        return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
+    return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
+
+
 @pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1], [257, 3]])
-def test_backward_plan_covers_every_key_and_query_tile_once(lengths):
-    """kv items (dK/dV of 128 keys) and q items (dQ of 128 queries), one per head each."""
-    hq, hkv = 12, 2
-    cu, items = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
-    kv_seen, q_seen = set(), set()
+@pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (12, 12)])
+@pytest.mark.parametrize("kind", [_lib.VA_PLAN_BWD, _lib.VA_PLAN_BWD_HEADS,
+                                  _lib.VA_PLAN_BWD_PAIRS])
+def test_backward_plan_covers_every_key_and_query_tile_once(lengths, hq, hkv, kind):
+    """kv items (dK/dV of 128 keys) and q items (dQ of 128 queries) cover every (tile, head) once:
+    q items one head each, kv items one head (heads plans) or two heads of one GQA group, the
+    last head of an odd group alone (pairs plans)."""
+    g = hq // hkv
+    bound = 2 * (-(-sum(lengths) // 128) + len(lengths)) * hq
+    pairs = g > 1 and (kind == _lib.VA_PLAN_BWD_PAIRS or
+                       (kind == _lib.VA_PLAN_BWD and bound >= _lib.VA_BWD_PAIR_MIN_ITEMS))
+    cu, items = plan(lengths, hq, hkv, kind)
+    kv_seen, q_seen = [], []
     for a, doc_end, doc_start, w in items.tolist():
-        kind, h = w >> 24, w & 0xffffff
-        assert 0 <= h < hq and kind in (0, 1)
+        item_kind, pair, h = w >> 24, (w >> 20) & 15, w & HEAD_MASK
+        assert 0 <= h < hq and item_kind in (0, 1) and pair in (0, 1)
         d = int(np.searchsorted(cu, doc_start, side="right")) - 1
         assert cu[d] == doc_start and cu[d + 1] == doc_end
         assert doc_start <= a < doc_end and (a - doc_start) % 128 == 0
-        (kv_seen if kind == 0 else q_seen).add((a, h))
-    expected = {(t, h) for s, e in zip(cu[:-1], cu[1:]) for t in range(s, e, 128)
-                for h in range(hq)}
-    assert kv_seen == expected and q_seen == expected
-    assert len(items) == 2 * len(expected)
+        if item_kind == 1:
+            assert pair == 0
+            q_seen.append((a, h))
+            continue
+        if pair:
+            assert pairs and (h % g) % 2 == 0 and (h % g) + 1 < g
+            kv_seen += [(a, h), (a, h + 1)]
+        else:
+            assert not pairs or h % g == g - 1, "pair plans keep only an odd group's last head"
+            kv_seen.append((a, h))
+    expected = sorted((t, h) for s, e in zip(cu[:-1], cu[1:]) for t in range(s, e, 128)
+                      for h in range(hq))
+    assert sorted(kv_seen) == expected and sorted(q_seen) == expected
+    n_kv = len(expected) // hq * hkv * ((g + 1) // 2 if pairs else g)
+    assert len(items) == n_kv + len(expected)
+    if pairs:
+        def per_combo(key):  # a group's pair items, the odd group's single, or both at one work
+            a, e, s, item_kind, _grp, work = key
+            if item_kind == 1:
+                return g
+            single = bwd_work(a, e, s, 0)
+            pair = bwd_work(a, e, s, 1 << 20)
+            if g % 2 == 0:
+                return g // 2
+            if pair == single:
+                return (g + 1) // 2
+            return 1 if work == single else g // 2
+        check_xcd_order(items, hq, hkv, bwd_work, per_combo)
+    else:
+        check_xcd_order(items, hq, hkv, bwd_work)
 
-    def work(a, e, s, w):  # the planner's measure: MFMAs per wave per step pair + item cost
-        if w >> 24 == 0:
-            return ((e - a + 31) // 32 + 1) // 2 * 32 + 39
-        return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
-    check_xcd_order(items, hq, hkv, work)
+
+@pytest.mark.parametrize("lengths,pairs", [([512] * 4, False), ([64, 37, 50, 12], False),
+                                           ([4096, 4096], True), ([180] * 45, True)])
+def test_backward_plan_takes_pairs_when_the_list_is_long(lengths, pairs):
+    """VA_PLAN_BWD is the heads plan below VA_BWD_PAIR_MIN_ITEMS per-head items (by the
+    host-known bound 2 (ceil(N / 128) + n_docs) Hq) and the pairs plan from there on."""
+    hq, hkv = 12, 2
+    n = sum(lengths)
+    bound = 2 * (-(-n // 128) + len(lengths)) * hq
+    assert (bound >= _lib.VA_BWD_PAIR_MIN_ITEMS) == pairs
+    _, auto = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
+    _, fixed = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD_PAIRS if pairs else _lib.VA_PLAN_BWD_HEADS)
+    assert np.array_equal(auto, fixed)
 
 
 def test_plan_rejects_bad_cu_seqlens():
@@ -191,7 +245,8 @@ def test_product_path_refuses_cpu_tensors():
 
 @pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1, 1, 1], [129, 0, 300],
                                      [4096, 17], [127, 128, 129]])
-@pytest.mark.parametrize("kind", [_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD])
+@pytest.mark.parametrize("kind", [_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD, _lib.VA_PLAN_BWD_HEADS,
+                                  _lib.VA_PLAN_BWD_PAIRS])
 def test_device_plan_capacity_bounds_the_host_plan(lengths, kind):
     """va_plan_capacity, from host-known sizes only, is never below the real item count."""
     hq = 12

@@ -124,6 +124,40 @@ def test_many_item_forward_matches_oracle(lengths, hq, hkv, dtype):
     check_all(out.cpu(), (dq.cpu(), dk.cpu(), dv.cpu()), ref, dtype, n, hq)
 
 
+class _Plan:
+    """A plan object for attention_forward / attention_backward from explicit item lists."""
+
+    def __init__(self, fwd, bwd, total):
+        self.fwd_items, self.n_fwd = fwd, fwd.shape[0]
+        self.bwd_items, self.n_bwd = bwd, bwd.shape[0]
+        self.total = total
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
+def test_pair_backward_matches_oracle(lengths, hq, hkv, dtype):
+    """The backward plan with two query heads per kv item (VA_PLAN_BWD_PAIRS, what VA_PLAN_BWD
+    takes for long lists), forced on small cases: dQ/dK/dV against the oracle, and bitwise equal
+    over two runs."""
+    qk = 3.0 if dtype == "peaky" else 1.0
+    dtype = torch.bfloat16 if dtype == "peaky" else dtype
+    banner("pair backward", lengths, hq, hkv, dtype, qk)
+    q, k, v, do = wl.make_inputs(lengths, hq, hkv, dtype, seed=sum(lengths) + 2, qk_scale=qk)
+    n = sum(lengths)
+    dev = torch.device("cuda")
+    base = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
+    cu = np.concatenate([[0], np.cumsum([x for x in lengths if x])]).astype(np.int32)
+    pair_items = torch.from_numpy(att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_BWD_PAIRS))
+    plan = _Plan(base.fwd_items[: base.n_fwd], pair_items.to(dev), n)
+    qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
+    out, lse = att.attention_forward(qd, kd, vd, plan, SCALE)
+    runs = [att.attention_backward(dod, qd, kd, vd, out, lse, plan, SCALE) for _ in range(2)]
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    ref = oracle(q, k, v, do, lengths)
+    check_all(out.cpu(), tuple(t.cpu() for t in runs[0]), ref, dtype, n, hq)
+
+
 @pytest.mark.parametrize("name", sorted(GOLDEN))
 def test_golden_vectors(name):
     z = load_golden(name)
@@ -407,29 +441,38 @@ def test_packed_attention_matches_oracle(dtype):
         assert r <= tol["g"], (name, r)
 
 
+HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | pair << 20 | head
+
+
 def plan_work(kind, a, e, s, w):
-    """The planners' work measure of an item: keys visited (forward); MFMAs per wave per step
-    pair plus the item's fixed cost (backward)."""
+    """The planners' work measure of an item: keys visited (forward); MFMAs per wave per
+    iteration plus the item's fixed cost (backward; a pair item's halves take every step)."""
     if kind == 0:
         return min(a + 128, e) - s
     if w >> 24 == 0:
-        return ((e - a + 31) // 32 + 1) // 2 * 32 + 39
+        steps = (e - a + 31) // 32
+        return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
     return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
 
 
-def check_device_xcd_layout(items, kind, hq, hkv):
-    """The G items of one (tile, kind, GQA group) sit a constant stride apart, at most 8 (one
-    XCD), and the groups come longest first by the work measure in buckets of 8."""
+def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
+    """The items of one (tile, kind, GQA group) sit a constant stride apart, at most 8 (one XCD),
+    and the groups come longest first by the work measure in buckets of 8. Empty items (the
+    rows a pair plan leaves free) are skipped."""
     g = hq // hkv
     combos = {}
     for pos, (a, e, s, w) in enumerate(items.tolist()):
-        combos.setdefault((a, e, s, w >> 24, (w & 0xFFFFFF) // g), []).append(pos)
+        if (a, e, s, w) == (0, 0, 0, 0):
+            continue
+        combos.setdefault((a, e, s, w >> 24, (w & HEAD_MASK) // g), []).append((pos, w))
     firsts = []
-    for key, pos in combos.items():
-        assert len(pos) == g, key
+    for key, entries in combos.items():
+        pos = [p for p, _ in entries]
+        assert len(pos) == (g if not pairs or key[3] == 1 else (g + 1) // 2), key
         steps = {b - a for a, b in zip(pos, pos[1:])}
         assert len(steps) <= 1 and all(0 < x <= 8 for x in steps), (key, pos)
-        firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], key[3] << 24) // 8))
+        w0 = (key[3] << 24) | ((1 << 20) if pairs and key[3] == 0 and g > 1 else 0)
+        firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], w0) // 8))
     work = [w for _, w in sorted(firsts)]
     assert work == sorted(work, reverse=True)
 
@@ -463,6 +506,19 @@ def test_device_plan_matches_host_plan(lengths):
         torch.cuda.synchronize()
         again = again.cpu().numpy()[:count]
         assert sorted(map(tuple, again.tolist())) == sorted(map(tuple, got.tolist()))
+    # the pair plan (two heads per kv item) from the device cu_seqlens: the host pair plan's items
+    # plus empty items (the free rows of the kv blocks and the slots past the real items)
+    count = dplan.n_bwd
+    pair_items = torch.empty_like(dplan.bwd_items)
+    att.check(att.lib().va_plan_build_device(dplan.cu.data_ptr(), len(lengths), n, hq, hkv,
+                                             att._lib.VA_PLAN_BWD_PAIRS, pair_items.data_ptr(),
+                                             count, att._stream()), "va_plan_build_device")
+    torch.cuda.synchronize()
+    got = pair_items.cpu().numpy()[:count]
+    host = att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_BWD_PAIRS)
+    real = [tuple(x) for x in got.tolist() if any(x)]
+    assert sorted(real) == sorted(map(tuple, host.tolist()))
+    check_device_xcd_layout(got, 1, hq, hkv, pairs=True)
 
 
 def test_device_lengths_plan_is_rebuilt_inside_a_captured_graph():
