@@ -331,7 +331,9 @@ __device__ __forceinline__ void bwd_kv_item(
 }
 
 // --------------------------------------------------------------------------------------------
-// q item: dQ of 128 queries for one query head.
+// q item: dQ of 128 queries for one query head, or (pair items) for two query heads h, h + 1 of
+// one GQA group: then half j takes head h + j over both tiles of every pair, so the halves share
+// the K/V tiles, never exchange dQ, and each writes all 128 columns of its head.
 // --------------------------------------------------------------------------------------------
 template <class E>
 __device__ __forceinline__ void bwd_q_item(
@@ -342,6 +344,7 @@ __device__ __forceinline__ void bwd_q_item(
     float scale, float scale_log2, float* stat_f) {
   using namespace bwd;
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kHeadMask;
+  const bool pair = (it.w >> 20) & 1;
   const int kvh = h / (hq / hkv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
   const int half = wave / NS, strip = wave % NS;
@@ -378,41 +381,46 @@ __device__ __forceinline__ void bwd_q_item(
   // document end read as zeros), staged in LDS after the two K / V stages; O only for delta =
   // rowsum(dO * O), reduced over the 16 lanes of a row. Each lane then reads its query's Q and
   // dO rows as B operands (k slots = d), lse and delta from the 256-float stat area.
+  // A pair item stages its second head's Q / dO in the K / V stages (free until the first pair
+  // is stored, after every wave has read its rows back) and its lse / delta in stat_f[2 QB ..).
   constexpr int QT_OFF = Q_HALFS;
   static_assert(Q_HALFS + 2 * QB * LD <= HALFS, "Q / dO tiles of a q item fit in LDS");
-  static_assert(2 * QB <= 2 * 2 * 2 * BQ, "lse / delta of a q item fit in the stat area");
-  {
-    const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(h + 1) * D) * 2;
+  static_assert(2 * QB * LD <= Q_HALFS, "a second head's Q / dO tiles fit in the K / V stages");
+  auto stage_head = [&](int hh, int off_q, float* st) {
+    const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(hh + 1) * D) * 2;
     const brsrc rq = make_rsrc(q + (long)q0 * qrow, bytes);
     const brsrc rd = make_rsrc(dout + (long)q0 * qrow, bytes);
     const brsrc ro = make_rsrc(out + (long)q0 * qrow, bytes);
     u32x4 xq[QB / 32], xd[QB / 32], xo[QB / 32];
 #pragma unroll
     for (int i = 0; i < QB / 32; ++i) {
-      const int off = ((srow + 32 * i) * (int)qrow + h * D + scol) * 2;
+      const int off = ((srow + 32 * i) * (int)qrow + hh * D + scol) * 2;
       xq[i] = bload16(rq, off);
       xd[i] = bload16(rd, off);
       xo[i] = bload16(ro, off);
     }
     if (tid < QB)
-      stat_f[tid] = q0 + tid < doc_end ? lse[(long)h * n_tokens + q0 + tid] * kLog2e : INFINITY;
+      st[tid] = q0 + tid < doc_end ? lse[(long)hh * n_tokens + q0 + tid] * kLog2e : INFINITY;
 #pragma unroll
     for (int i = 0; i < QB / 32; ++i) {
-      st128(smem + QT_OFF + (srow + 32 * i) * LD + scol, xq[i]);
-      st128(smem + QT_OFF + QB * LD + (srow + 32 * i) * LD + scol, xd[i]);
+      st128(smem + off_q + (srow + 32 * i) * LD + scol, xq[i]);
+      st128(smem + off_q + QB * LD + (srow + 32 * i) * LD + scol, xd[i]);
       float d = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) d = E::dot2(xo[i][w], xd[i][w], d);
       d = sum_rows16(d);
-      if ((tid & 15) == 0) stat_f[QB + srow + 32 * i] = d;
+      if ((tid & 15) == 0) st[QB + srow + 32 * i] = d;
     }
-  }
+  };
+  stage_head(h, QT_OFF, stat_f);
+  if (pair) stage_head(h + 1, 0, stat_f + 2 * QB);
 
-  // LDS read bases: K / V rows as A operands (rows = keys through perm32, k = d); K^T through
-  // transposed reads with the column order that keeps output registers d-contiguous.
-  const int ka_read = (2 * half) * ROWT + perm32(l32) * LD + 8 * hi;
-  const int va_read = (2 * half + 1) * ROWT + perm32(l32) * LD + 8 * hi;
-  const int kt_read = (2 * half) * ROWT + (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) +
+  // LDS read bases inside a tile slot (K at 2 slot, V at 2 slot + 1): K / V rows as A operands
+  // (rows = keys through perm32, k = d); K^T through transposed reads with the column order that
+  // keeps output registers d-contiguous.
+  const int ka_read = perm32(l32) * LD + 8 * hi;
+  const int va_read = ROWT + perm32(l32) * LD + 8 * hi;
+  const int kt_read = (8 * hi + 2 * (src >> 2)) * LD + 16 * (grp & 1) +
                       4 * ((((src & 3) & 1) << 1) | ((src & 3) >> 1));
 
   f32x16 dqacc[4];
@@ -420,27 +428,36 @@ __device__ __forceinline__ void bwd_q_item(
   for (int db = 0; db < 4; ++db) dqacc[db] = f32x16{};
 
   if (half) __builtin_amdgcn_s_setprio(1);  // see the forward kernel: issue ties between halves
-  store_pair(0);
+  if (!pair) store_pair(0);
   __syncthreads();
   u32x4 qf[8], df[8];
+  const bool second = pair && half;  // this half's head was staged in the K / V stages
+  {
+    const int off_q = second ? 0 : QT_OFF;
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
-    qf[kk] = ld128(smem + QT_OFF + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
-    df[kk] = ld128(smem + QT_OFF + QB * LD + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
+    for (int kk = 0; kk < 8; ++kk) {
+      qf[kk] = ld128(smem + off_q + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
+      df[kk] = ld128(smem + off_q + QB * LD + (32 * strip + l32) * LD + 16 * kk + 8 * hi);
+    }
   }
-  const float lse2 = stat_f[32 * strip + l32], dlt = stat_f[QB + 32 * strip + l32];
+  const float* st = stat_f + (second ? 2 * QB : 0);
+  const float lse2 = st[32 * strip + l32], dlt = st[QB + 32 * strip + l32];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
     settle(qf[kk]);
     settle(df[kk]);
   }
-  for (int p = 0; p < n_pairs; ++p) {
-    const int stage = p & 1;
-    if (p + 1 < n_pairs) gload_pair(p + 1);
-    const int t = 2 * p + half;
+  if (pair) {  // every wave holds its rows: the first K / V pair may now take the stages
+    __syncthreads();
+    store_pair(0);
+    __syncthreads();
+  }
+  const int my_head = pair ? h + half : h;
+  // Tile t of the stage's slot `slot` (0: K0 V0, 1: K1 V1): S^T, dP^T, dS^T, dQ^T += K^T dS^T.
+  auto qtile = [&](int stage, int t, int slot) {
     const int kv0 = doc_start + t * BT;
     if (t < n_tiles && kv0 <= wq0 + 31) {
-      const lds_u16* base = smem + stage * Q_PAIR;
+      const lds_u16* base = smem + stage * Q_PAIR + 2 * slot * ROWT;
       // S^T = K Q^T and dP^T = V dO^T: 16 MFMAs, the K / V operand read 3 MFMAs ahead.
       f32x16 sacc = f32x16{}, pacc = f32x16{};
       auto opa = [&](int i) {  // MFMA i: kk = i >> 1, S (i even) or dP (i odd)
@@ -485,8 +502,44 @@ __device__ __forceinline__ void bwd_q_item(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+  };
+  for (int p = 0; p < n_pairs; ++p) {
+    const int stage = p & 1;
+    if (p + 1 < n_pairs) gload_pair(p + 1);
+    if (pair) {
+      qtile(stage, 2 * p, 0);
+      qtile(stage, 2 * p + 1, 1);
+    } else {
+      qtile(stage, 2 * p + half, half);
+    }
     if (p + 1 < n_pairs) store_pair(stage ^ 1);
     __syncthreads();
+  }
+
+  if (pair) {
+    // Each half holds its head's whole dQ^T: 64 columns at a time through this wave's own row
+    // tile (the LDS is free after the loop's last barrier), scaled.
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    lds_u16* tile = smem + wv * 32 * (8 * 8 + 8);
+    static_assert(NW * 32 * (8 * 8 + 8) <= HALFS, "per-wave row tiles fit in LDS");
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      u32x4 w[4];
+#pragma unroll
+      for (int db2 = 0; db2 < 2; ++db2)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const f32x16& a = dqacc[2 * c2 + db2];
+          w[2 * db2 + c] = pack8<E>(a[8 * c] * scale, a[8 * c + 1] * scale, a[8 * c + 2] * scale,
+                                    a[8 * c + 3] * scale, a[8 * c + 4] * scale,
+                                    a[8 * c + 5] * scale, a[8 * c + 6] * scale,
+                                    a[8 * c + 7] * scale);
+        }
+      store_rows32<8>(tile, w, lane,
+                      [&](int r) { return dq + (long)(wq0 + r) * qrow + my_head * D + 64 * c2; },
+                      doc_end - wq0);
+    }
+    return;
   }
 
   // The halves swap partial dQ^T columns (16-byte chunks, same lane order): half h finishes
@@ -544,22 +597,23 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     uint16_t* __restrict__ dv_part, int n_tokens, float scale, float scale_log2) {
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
+  __shared__ __attribute__((aligned(16))) float qstat[4 * bwd::QB];  // q items: [head][lse|del]
   lds_u16* smem = (lds_u16*)smem_raw;
   const int4 it = items[blockIdx.x];
   // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
   // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
   const int kind = it.w >> 24, h = it.w & bwd::kHeadMask, pair = (it.w >> 20) & 15;
-  // Pair items (kv only) take heads h, h + 1 of one GQA group.
+  // Pair items take heads h, h + 1 of one GQA group.
   if (it.x >= it.y || it.z < 0 || it.x < it.z || it.y > n_tokens || h >= hq ||
       (kind != bwd::kKindKV && kind != bwd::kKindQ) || pair > 1 ||
-      (pair && (kind != bwd::kKindKV || h + 1 >= hq || h / (hq / hkv) != (h + 1) / (hq / hkv))))
+      (pair && (h + 1 >= hq || h / (hq / hkv) != (h + 1) / (hq / hkv))))
     return;
   if (kind == bwd::kKindKV) {
     bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,
                    scale, scale_log2);
   } else {
     bwd_q_item<E>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale, scale_log2,
-                  &stat[0][0][0][0]);
+                  qstat);
   }
 }
 

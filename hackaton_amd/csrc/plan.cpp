@@ -85,8 +85,13 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
       for (int32_t q0 = s; q0 < e; q0 += va::kBwdBlockM) {
         const int64_t kv_end = std::min<int64_t>((int64_t)q0 + va::kBwdBlockM, e);
         const int64_t tiles = (kv_end - s + va::kBwdTileK - 1) / va::kBwdTileK;
-        const int64_t work = (tiles + 1) / 2 * 24 + kQItemCost;
-        for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, (1 << 24) | h, work});
+        for (int32_t g = 0; g < hkv; ++g)
+          for (int32_t r = 0; r < rows; ++r) {
+            const bool pair = pairs && 2 * r + 1 < group;
+            const int32_t h = g * group + (pairs ? 2 * r : r);
+            const int64_t work = (tiles + 1) / 2 * (pair ? 48 : 24) + kQItemCost;
+            items.push_back({q0, e, s, (1 << 24) | (pair ? va::kItemPairBit : 0) | h, work});
+          }
       }
     }
   }
@@ -133,7 +138,7 @@ std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
 int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind) {
   int64_t n = 0;
   const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
-  const int64_t kv_per_tile = pairs ? (int64_t)hkv * ((hq / hkv + 1) / 2) : hq;
+  const int64_t kv_per_tile = pairs ? (int64_t)hkv * ((hq / hkv + 1) / 2) : hq;  // per kind
   for (int32_t i = 0; i < n_docs; ++i) {
     const int64_t len = (int64_t)cu[i + 1] - cu[i];
     if (len <= 0) continue;
@@ -141,7 +146,7 @@ int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv, 
       n += (len + va::kFwdBlockM - 1) / va::kFwdBlockM * hq;
     } else {
       n += (len + va::kBwdBlockN - 1) / va::kBwdBlockN * kv_per_tile;
-      n += (len + va::kBwdBlockM - 1) / va::kBwdBlockM * hq;
+      n += (len + va::kBwdBlockM - 1) / va::kBwdBlockM * kv_per_tile;
     }
   }
   return n;

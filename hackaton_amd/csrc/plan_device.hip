@@ -179,7 +179,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
     } else {
       const long kv_end = min(s + (long)(t + 1) * kTile, e);
       const long tiles = (kv_end - s + kBwdTileK - 1) / kBwdTileK;
-      work = (tiles + 1) / 2 * 24 + kPlanQItemCost;
+      work = (tiles + 1) / 2 * (pairs ? 48 : 24) + kPlanQItemCost;
     }
     const long b = work >> 3;
     return (int)(b >= kBuckets ? kBuckets - 1 : b);
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   __syncthreads();
   // Candidate at sorted position `pos` holds combos pos * Hkv + g (g = GQA group); combo j sits
   // in column j % 8 of block j / 8, which spans 8 G slots (fewer columns in the last block);
-  // head r of the group goes to row r. In a pair plan a kv combo's row r < ceil(G / 2) holds the
+  // head r of the group goes to row r. In a pair plan a combo's row r < ceil(G / 2) holds the
   // item of heads 2 r, 2 r + 1 (the last head of an odd group alone) and its other rows stay
   // empty items.
   const long n_combos = (long)n_cand * hkv;
@@ -227,10 +227,11 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       for (int r = 0; r < group; ++r) {
         const long slot = blk * kXcds * group + r * ncols + col;
         int4 item = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
-        if (pairs && !is_q) {
+        if (pairs) {
           const int h2 = 2 * r;
           item = h2 < group ? int4{s + t * kTile, e, s,
-                                   (h2 + 1 < group ? kItemPairBit : 0) | (g * group + h2)}
+                                   (is_q << 24) | (h2 + 1 < group ? kItemPairBit : 0) |
+                                       (g * group + h2)}
                             : int4{0, 0, 0, 0};
         }
         if (slot < capacity) items[slot] = item;

@@ -23,7 +23,7 @@ constexpr int kPlanMaxDocs = 8192;  // documents a device-built plan takes (LDS-
 // wave per step pair: 32 per kv step pair, 24 per q tile pair (from in-graph item durations).
 constexpr int kPlanKvItemCost = 39;
 constexpr int kPlanQItemCost = 30;
-// VA_PLAN_BWD takes two query heads per kv item (pair items, Hq > Hkv) once the per-head list
+// VA_PLAN_BWD takes two query heads per item (pair items, Hq > Hkv) once the per-head list
 // would be this long (2 (ceil(N / 128) + n_docs) Hq items: every CU then holds several).
 constexpr int kBwdPairMinItems = 1024;
 constexpr int kItemPairBit = 1 << 20;  // item word: kind << 24 | pair << 20 | head

@@ -62,15 +62,15 @@ int32_t va_head_dim(void);
 
 /* ---- work plan (host only; no GPU call) ------------------------------------------------------
  * Work items for the forward (kind VA_PLAN_FWD: one per 128-query tile x query head) or the
- * backward (one per 128-query tile x query head for dQ, and for dK/dV one per 128-key tile x
- * query head (VA_PLAN_BWD_HEADS) or one per 128-key tile x pair of query heads of one GQA group,
- * the last head of an odd group alone (VA_PLAN_BWD_PAIRS); VA_PLAN_BWD takes pairs when Hq > Hkv
+ * backward (one per 128-key tile for dK/dV and one per 128-query tile for dQ, each x query
+ * head (VA_PLAN_BWD_HEADS) or x pair of query heads of one GQA group, the last head of an odd
+ * group alone (VA_PLAN_BWD_PAIRS); VA_PLAN_BWD takes pairs when Hq > Hkv
  * and the per-head list would hold 2 (ceil(n_tokens / 128) + n_docs) Hq >= VA_BWD_PAIR_MIN_ITEMS
  * items, heads otherwise) over the documents of cu_seqlens, longest first. The items of one tile
  * and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the heads
  * sharing K/V run on one XCD and share its L2. Fully masked causal tiles and cross-document tiles
  * never appear. Every plan kind gives the same outputs up to rounding (a pair item sums a head's
- * query steps in one sequence instead of two halves); each is deterministic.
+ * steps or tiles in one sequence instead of two halves); each is deterministic.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
 int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                  int64_t* n_items);

@@ -100,7 +100,7 @@ def bwd_work(a, e, s, w):
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
         return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
-    return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
+    return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * (48 if (w >> 20) & 1 else 24) + 30
 
 
 @pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1], [257, 3]])
@@ -109,8 +109,8 @@ def bwd_work(a, e, s, w):
                                   _lib.VA_PLAN_BWD_PAIRS])
 def test_backward_plan_covers_every_key_and_query_tile_once(lengths, hq, hkv, kind):
     """kv items (dK/dV of 128 keys) and q items (dQ of 128 queries) cover every (tile, head) once:
-    q items one head each, kv items one head (heads plans) or two heads of one GQA group, the
-    last head of an odd group alone (pairs plans)."""
+    one head each (heads plans) or two heads of one GQA group, the last head of an odd group
+    alone (pairs plans)."""
     g = hq // hkv
     bound = 2 * (-(-sum(lengths) // 128) + len(lengths)) * hq
     pairs = g > 1 and (kind == _lib.VA_PLAN_BWD_PAIRS or
@@ -123,28 +123,23 @@ def test_backward_plan_covers_every_key_and_query_tile_once(lengths, hq, hkv, ki
         d = int(np.searchsorted(cu, doc_start, side="right")) - 1
         assert cu[d] == doc_start and cu[d + 1] == doc_end
         assert doc_start <= a < doc_end and (a - doc_start) % 128 == 0
-        if item_kind == 1:
-            assert pair == 0
-            q_seen.append((a, h))
-            continue
+        seen = kv_seen if item_kind == 0 else q_seen
         if pair:
             assert pairs and (h % g) % 2 == 0 and (h % g) + 1 < g
-            kv_seen += [(a, h), (a, h + 1)]
+            seen += [(a, h), (a, h + 1)]
         else:
             assert not pairs or h % g == g - 1, "pair plans keep only an odd group's last head"
-            kv_seen.append((a, h))
+            seen.append((a, h))
     expected = sorted((t, h) for s, e in zip(cu[:-1], cu[1:]) for t in range(s, e, 128)
                       for h in range(hq))
     assert sorted(kv_seen) == expected and sorted(q_seen) == expected
-    n_kv = len(expected) // hq * hkv * ((g + 1) // 2 if pairs else g)
-    assert len(items) == n_kv + len(expected)
+    n_kind = len(expected) // hq * hkv * ((g + 1) // 2 if pairs else g)
+    assert len(items) == 2 * n_kind
     if pairs:
         def per_combo(key):  # a group's pair items, the odd group's single, or both at one work
             a, e, s, item_kind, _grp, work = key
-            if item_kind == 1:
-                return g
-            single = bwd_work(a, e, s, 0)
-            pair = bwd_work(a, e, s, 1 << 20)
+            single = bwd_work(a, e, s, item_kind << 24)
+            pair = bwd_work(a, e, s, (item_kind << 24) | (1 << 20))
             if g % 2 == 0:
                 return g // 2
             if pair == single:

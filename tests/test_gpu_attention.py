@@ -135,7 +135,7 @@ class _Plan:
 
 @pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
 def test_pair_backward_matches_oracle(lengths, hq, hkv, dtype):
-    """The backward plan with two query heads per kv item (VA_PLAN_BWD_PAIRS, what VA_PLAN_BWD
+    """The backward plan with two query heads per kv and q item (VA_PLAN_BWD_PAIRS, what VA_PLAN_BWD
     takes for long lists), forced on small cases: dQ/dK/dV against the oracle, and bitwise equal
     over two runs."""
     qk = 3.0 if dtype == "peaky" else 1.0
@@ -452,7 +452,7 @@ def plan_work(kind, a, e, s, w):
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
         return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
-    return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * 24 + 30
+    return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * (48 if (w >> 20) & 1 else 24) + 30
 
 
 def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
@@ -468,10 +468,10 @@ def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
     firsts = []
     for key, entries in combos.items():
         pos = [p for p, _ in entries]
-        assert len(pos) == (g if not pairs or key[3] == 1 else (g + 1) // 2), key
+        assert len(pos) == (g if not pairs else (g + 1) // 2), key
         steps = {b - a for a, b in zip(pos, pos[1:])}
         assert len(steps) <= 1 and all(0 < x <= 8 for x in steps), (key, pos)
-        w0 = (key[3] << 24) | ((1 << 20) if pairs and key[3] == 0 and g > 1 else 0)
+        w0 = (key[3] << 24) | ((1 << 20) if pairs and g > 1 else 0)
         firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], w0) // 8))
     work = [w for _, w in sorted(firsts)]
     assert work == sorted(work, reverse=True)
