@@ -315,7 +315,9 @@ class Workload:
                 s.out.data_ptr(), s.lse.data_ptr(), p.bwd_items.data_ptr(), p.n_bwd, s.n,
                 self.hq, self.hkv, 128, self.scale, self.dcode, s.dq.data_ptr(), s.dk.data_ptr(),
                 s.dv.data_ptr(), s.ws.data_ptr(), s.ws.numel(), stream)
-        if stage < 0:
+        if stage < 0 and not self.gqa_sum_launched():  # the plan's group items write dK/dV
+            self._lib.check(self.lib.va_bwd_stage(self._lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
+        elif stage < 0:
             self._lib.check(self.lib.va_bwd(*argv), "va_bwd")
         else:
             self._lib.check(self.lib.va_bwd_stage(stage, *argv), "va_bwd_stage")
@@ -370,7 +372,8 @@ class Workload:
         return out
 
     def gqa_sum_launched(self):
-        return self.hq != self.hkv
+        """The GQA sum runs unless Hq == Hkv or group items cover every key tile of the plan."""
+        return self.plan.bwd_finish
 
 
 def time_config(cfg, reps):

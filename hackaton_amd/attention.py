@@ -88,21 +88,37 @@ def _cu_seqlens(lengths, device):
 
 
 class Plan:
-    """Device work lists of the forward and backward kernels for one (cu_seqlens, Hq, Hkv)."""
+    """Device work lists of the forward and backward kernels for one (cu_seqlens, Hq, Hkv). The
+    backward list takes GQA group items where they do not lengthen it (VA_PLAN_BWD_GROUPS); a
+    backward that leaves per-head dK/dV partials to its caller takes `partial_bwd()`, the list
+    without them."""
 
-    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "offsets")
+    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "offsets", "_hq", "_hkv",
+                 "_part", "bwd_finish")
 
     def __init__(self, offsets, hq, hkv, device):
         cu = np.ascontiguousarray(np.asarray(offsets, dtype=np.int32))
         self.offsets = tuple(int(x) for x in cu)
         self.total = int(cu[-1])
-        items = []
-        for kind in (_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD):
-            items.append(build_plan_host(cu, hq, hkv, kind))
-        host_fwd, host_bwd = items
+        self._hq, self._hkv = hq, hkv
+        bwd_kind = _lib.VA_PLAN_BWD_GROUPS if hq > hkv else _lib.VA_PLAN_BWD
+        host_fwd = build_plan_host(cu, hq, hkv, _lib.VA_PLAN_FWD)
+        host_bwd = build_plan_host(cu, hq, hkv, bwd_kind)
         self.n_fwd, self.n_bwd = host_fwd.shape[0], host_bwd.shape[0]
         self.fwd_items = torch.from_numpy(host_fwd).to(device)
         self.bwd_items = torch.from_numpy(host_bwd).to(device)
+        self._part = None if hq > hkv else (self.bwd_items, self.n_bwd)
+        # whether the backward needs its GQA sum: not when group items cover every key tile
+        kv = host_bwd[(host_bwd[:, 3] >> 24) == 0]
+        self.bwd_finish = hq > hkv and not bool(((kv[:, 3] >> 21) & 1).all())
+
+    def partial_bwd(self):
+        """(items, n) of the backward list without group items (built on first use)."""
+        if self._part is None:
+            cu = np.asarray(self.offsets, dtype=np.int32)
+            host = build_plan_host(cu, self._hq, self._hkv, _lib.VA_PLAN_BWD)
+            self._part = (torch.from_numpy(host).to(self.bwd_items.device), host.shape[0])
+        return self._part
 
 
 def build_plan_host(cu, hq, hkv, kind):
@@ -121,11 +137,15 @@ def build_plan_host(cu, hq, hkv, kind):
 
 
 class DevicePlan:
-    """Work lists and cu_seqlens built on the device from device lengths by one launch
-    (va_plan_build_device_lengths): no host read. Each list has the capacity that the host-known
+    """Work lists and cu_seqlens built on the device from device lengths: no host read. One launch
+    (va_plan_build_device_lengths) builds cu_seqlens, the forward list and the backward list
+    without GQA group items; with Hq > Hkv a second (va_plan_build_device from that cu_seqlens)
+    builds the backward list with them (VA_PLAN_BWD_GROUPS), and the first one serves a backward
+    that leaves per-head partials to its caller. Each list has the capacity that the host-known
     sizes bound; its slots past the real items are empty items that the kernels skip."""
 
-    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "cu", "__weakref__")
+    __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "cu", "_part",
+                 "bwd_finish", "__weakref__")
 
     def __init__(self, lengths, n_tokens, hq, hkv):
         lengths = lengths.reshape(-1)
@@ -143,13 +163,25 @@ class DevicePlan:
             caps.append(int(cap[0]))
         self.n_fwd, self.n_bwd = caps
         self.fwd_items = torch.empty(max(self.n_fwd, 1), 4, dtype=torch.int32, device=dev)
-        self.bwd_items = torch.empty(max(self.n_bwd, 1), 4, dtype=torch.int32, device=dev)
+        part = torch.empty(max(self.n_bwd, 1), 4, dtype=torch.int32, device=dev)
         self.cu = torch.empty(n_docs + 1, dtype=torch.int32, device=dev)
         check(lib().va_plan_build_device_lengths(
             lengths.data_ptr() if n_docs else None, n_docs, n_tokens, hq, hkv,
-            self.fwd_items.data_ptr(), self.n_fwd, self.bwd_items.data_ptr(), self.n_bwd,
+            self.fwd_items.data_ptr(), self.n_fwd, part.data_ptr(), self.n_bwd,
             self.cu.data_ptr(), _stream()), "va_plan_build_device_lengths")
+        self._part = (part, self.n_bwd)
+        self.bwd_items = part
+        self.bwd_finish = hq > hkv  # the device list's group tiles are not known here
+        if hq > hkv and n_docs > 0:
+            self.bwd_items = torch.empty_like(part)
+            check(lib().va_plan_build_device(self.cu.data_ptr(), n_docs, n_tokens, hq, hkv,
+                                             _lib.VA_PLAN_BWD_GROUPS, self.bwd_items.data_ptr(),
+                                             self.n_bwd, _stream()), "va_plan_build_device")
         self.cu._va_plan = self
+
+    def partial_bwd(self):
+        """(items, n) of the backward list without group items."""
+        return self._part
 
 
 def _capture_id():
@@ -245,10 +277,14 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
     else:
         dk = dv = None
     ws, offs = bwd_workspace(n, hq, hkv, query.device)
-    check(lib().va_bwd(_ptr(grad), _ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
-                       _ptr(plan.bwd_items), plan.n_bwd, n, hq, hkv, d, float(scale), dtype,
-                       _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws) if ws.numel() else None,
-                       ws.numel(), _stream()), "va_bwd")
+    items, n_items = (plan.bwd_items, plan.n_bwd) if outputs else plan.partial_bwd()
+    argv = (_ptr(grad), _ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
+            _ptr(items), n_items, n, hq, hkv, d, float(scale), dtype,
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws) if ws.numel() else None, ws.numel(), _stream())
+    if outputs and not getattr(plan, "bwd_finish", True):  # group items wrote every dK/dV row
+        check(lib().va_bwd_stage(_lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
+    else:
+        check(lib().va_bwd(*argv), "va_bwd")
     if outputs:
         return dq, dk, dv
     part = n * hq * d * 2

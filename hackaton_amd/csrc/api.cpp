@@ -11,7 +11,8 @@
 
 static_assert(va::kFwdLeanMinItems == VA_FWD_MANY_ITEMS, "forward kernel switch: header and kernels");
 static_assert(va::kBwdPairMinItems == VA_BWD_PAIR_MIN_ITEMS && VA_PLAN_BWD_HEADS == 2 &&
-                  VA_PLAN_BWD_PAIRS == 3,
+                  VA_PLAN_BWD_PAIRS == 3 && VA_PLAN_BWD_GROUPS == 4 &&
+                  VA_PLAN_BWD_GROUPS_ALL == 5,
               "backward plan kinds: header and planners");
 
 namespace va {
@@ -93,7 +94,8 @@ extern "C" int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t
   const int64_t part = round256(total_tokens * hq * head_dim * 2);
   offsets[0] = 0;     // per-query-head dK partials (N, Hq, D), element type
   offsets[1] = part;  // per-query-head dV partials
-  *bytes = 2 * part;
+  // then (N) uint32 row flags at 2 part: which rows a GQA group item finished itself
+  *bytes = 2 * part + round256(total_tokens * 4);
   return VA_OK;
 }
 
@@ -127,8 +129,9 @@ int bwd_checked(int32_t stage, const void* dout, const void* q, const void* k, c
   char* ws = static_cast<char*>(workspace);
   void* dk_part = direct ? dk : static_cast<void*>(ws + offs[0]);
   void* dv_part = direct ? dv : static_cast<void*>(ws + offs[1]);
+  uint32_t* flags = direct ? nullptr : reinterpret_cast<uint32_t*>(ws + 2 * offs[1]);
   va::BwdArgs a{dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, scale, dtype,
-                dq, dk_part, dv_part, dk, dv, (hipStream_t)stream};
+                dq, dk_part, dv_part, dk, dv, flags, (hipStream_t)stream};
   hipError_t e = stage < 0 ? va::launch_bwd(a) : va::launch_bwd_stage(a, stage);
   return e == hipSuccess ? VA_OK : hip_fail(e, "va_bwd launch");
 }

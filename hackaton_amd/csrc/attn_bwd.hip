@@ -60,12 +60,15 @@ __device__ __forceinline__ void bwd_kv_item(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ out,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
-    uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part, int n_tokens, int hq,
-    int hkv, float scale, float scale_log2) {
+    uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part, uint16_t* __restrict__ dk_out,
+    uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags, int n_tokens, int hq, int hkv,
+    float scale, float scale_log2) {
   using namespace bwd;
   const int k0 = it.x, doc_end = it.y, h = it.w & kHeadMask;
   const bool pair = (it.w >> 20) & 1;
-  const int kvh = h / (hq / hkv);
+  const bool all_heads = (it.w >> 21) & 1;  // group item: heads h .. h + G - 1 in sequence
+  const int G = hq / hkv;
+  const int kvh = h / G;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
   const int half = wave / NS, strip = wave % NS;
   const int src = lane & 15, grp = lane >> 4;
@@ -85,11 +88,18 @@ __device__ __forceinline__ void bwd_kv_item(
   }
 
   const int n_steps = (doc_end - k0 + BQ - 1) / BQ;
-  // Iterations of the step loop: a step pair of one head (the halves take alternate steps), or
-  // one step of each head of a pair item.
-  const int n_iter = pair ? n_steps : (n_steps + 1) / 2;
-  auto step_of = [&](int p, int j) { return pair ? p : 2 * p + j; };  // step of half j at p
-  auto head_of = [&](int j) { return pair ? h + j : h; };
+  // Units of work: (head, step) in head-major order, over one head or (group items) the G heads
+  // of the group. Iterations of the step loop: a pair of units (the halves take alternate units),
+  // or one step of each head of a pair item.
+  const int n_units = (all_heads ? G : 1) * n_steps;
+  const int n_iter = pair ? n_steps : (n_units + 1) / 2;
+  auto unit_of = [&](int p, int j) { return min(2 * p + j, n_units - 1); };  // clamped: loads
+  auto step_of = [&](int p, int j) { return pair ? p : unit_of(p, j) % n_steps; };
+  auto head_of = [&](int p, int j) { return pair ? h + j : h + unit_of(p, j) / n_steps; };
+  auto live = [&](int p, int j) {  // the unit exists and has queries at or after this strip's keys
+    if (!pair && 2 * p + j >= n_units) return false;
+    return kw0 <= k0 + step_of(p, j) * BQ + BQ - 1;
+  };
 
   // Staging of a step pair: thread chunk i is (step half i >> 1, tensor i & 1 = Q / dO), row
   // tid >> 4, 16-byte column tid & 15, through buffer loads bounded at the document end (rows past
@@ -104,7 +114,7 @@ __device__ __forceinline__ void bwd_kv_item(
   auto gload_pair = [&](int p) {
 #pragma unroll
     for (int sh = 0; sh < 2; ++sh) {
-      const int hs = head_of(sh);
+      const int hs = head_of(p, sh);
       const int qs0 = k0 + min(step_of(p, sh), n_steps - 1) * BQ;
       const long base = (long)qs0 * qrow;
       const long bytes = ((long)(doc_end - qs0 - 1) * qrow + (long)(hs + 1) * D) * 2;
@@ -116,7 +126,7 @@ __device__ __forceinline__ void bwd_kv_item(
     if (tid < 64) {  // raw value: scaled at the store, so that no wait follows the loads here
       const int sh = tid >> 5;
       st_row = k0 + min(step_of(p, sh), n_steps - 1) * BQ + (tid & 31);
-      st_lse = lse[(long)head_of(sh) * n_tokens + min(st_row, doc_end - 1)];
+      st_lse = lse[(long)head_of(p, sh) * n_tokens + min(st_row, doc_end - 1)];
     }
   };
   auto store_pair = [&](int stage) {
@@ -162,9 +172,8 @@ __device__ __forceinline__ void bwd_kv_item(
   for (int p = 0; p < n_iter; ++p) {
     const int stage = p & 1;
     if (p + 1 < n_iter) gload_pair(p + 1);
-    const int s = step_of(p, half);
-    const int qs0 = k0 + s * BQ;
-    if (s < n_steps && kw0 <= qs0 + BQ - 1) {
+    const int qs0 = k0 + step_of(p, half) * BQ;
+    if (live(p, half)) {
       const lds_u16* qs = smem + KV_OFF_Q + (stage * 2 + half) * ROWT;
       const lds_u16* dos = smem + KV_OFF_DO + (stage * 2 + half) * ROWT;
       // S = Q K^T and dP = dO V^T: 16 MFMAs, both operands of each read from LDS 3 MFMAs ahead.
@@ -267,7 +276,10 @@ __device__ __forceinline__ void bwd_kv_item(
   // The finished 32 x 128 tile goes out through this wave's own exchange slot (read just before,
   // by this wave only) as a row-major LDS tile, so that each 16-byte global store instruction
   // writes 4 whole rows instead of 32-byte pieces of 32 rows.
-  auto finish = [&](f32x16(&mine)[4], const f32x16(&other)[4], float mul, uint16_t* part) {
+  // Rows go to `part` at row stride `rs` heads, head `hd` (per-head partials, or a group item's
+  // dK/dV at Hkv width).
+  auto finish = [&](f32x16(&mine)[4], const f32x16(&other)[4], float mul, uint16_t* part, int rs,
+                    int hd) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -291,8 +303,12 @@ __device__ __forceinline__ void bwd_kv_item(
                                  x[8 * c + 4], x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]);
     }
     store_rows32<16>(reinterpret_cast<lds_u16*>(&xs[slot(half, 0, 0) - lane]), w, lane,
-                    [&](int r) { return part + ((long)(kw0 + r) * hq + h) * D; }, doc_end - kw0);
+                    [&](int r) { return part + ((long)(kw0 + r) * rs + hd) * D; }, doc_end - kw0);
   };
+  // The GQA sum reads which rows a group item finished (1) and which per-head partials hold (0):
+  // every key row belongs to one tile, whose group items or first head's items write its flags.
+  if (flags != nullptr && (all_heads || h % G == 0) && tid < BK && k0 + tid < doc_end)
+    flags[k0 + tid] = all_heads ? 1u : 0u;
   if (pair) {
     // Each half holds the whole dK/dV of its head: both go out through this wave's own row tile
     // (the LDS stages are free after the loop's last barrier), dK scaled.
@@ -326,8 +342,13 @@ __device__ __forceinline__ void bwd_kv_item(
     store(dvacc, 1.f, dv_part);
     return;
   }
-  if (half) finish(dvacc, dkacc, 1.f, dv_part);
-  else finish(dkacc, dvacc, scale, dk_part);
+  if (all_heads) {
+    if (half) finish(dvacc, dkacc, 1.f, dv_out, hkv, kvh);
+    else finish(dkacc, dvacc, scale, dk_out, hkv, kvh);
+  } else {
+    if (half) finish(dvacc, dkacc, 1.f, dv_part, hq, h);
+    else finish(dkacc, dvacc, scale, dk_part, hq, h);
+  }
 }
 
 // --------------------------------------------------------------------------------------------
@@ -594,7 +615,8 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, int hq, int hkv,
     const float* __restrict__ lse, uint16_t* __restrict__ dq, uint16_t* __restrict__ dk_part,
-    uint16_t* __restrict__ dv_part, int n_tokens, float scale, float scale_log2) {
+    uint16_t* __restrict__ dv_part, int n_tokens, float scale, float scale_log2,
+    uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags) {
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
   __shared__ __attribute__((aligned(16))) float qstat[4 * bwd::QB];  // q items: [head][lse|del]
@@ -602,15 +624,18 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
   const int4 it = items[blockIdx.x];
   // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
   // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
-  const int kind = it.w >> 24, h = it.w & bwd::kHeadMask, pair = (it.w >> 20) & 15;
-  // Pair items take heads h, h + 1 of one GQA group.
+  const int kind = it.w >> 24, h = it.w & bwd::kHeadMask, shape = (it.w >> 20) & 15;
+  // Pair items (shape 1) take heads h, h + 1 of one GQA group; group items (shape 2, kv only)
+  // every head of the group that starts at h, and need the Hkv-wide outputs.
+  const int G = hq / hkv;
   if (it.x >= it.y || it.z < 0 || it.x < it.z || it.y > n_tokens || h >= hq ||
-      (kind != bwd::kKindKV && kind != bwd::kKindQ) || pair > 1 ||
-      (pair && (h + 1 >= hq || h / (hq / hkv) != (h + 1) / (hq / hkv))))
+      (kind != bwd::kKindKV && kind != bwd::kKindQ) || shape > 2 ||
+      (shape == 1 && (h + 1 >= hq || h / G != (h + 1) / G)) ||
+      (shape == 2 && (kind != bwd::kKindKV || h % G != 0 || G < 2 || dk_out == nullptr)))
     return;
   if (kind == bwd::kKindKV) {
-    bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, n_tokens, hq, hkv,
-                   scale, scale_log2);
+    bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out, dv_out,
+                   flags, n_tokens, hq, hkv, scale, scale_log2);
   } else {
     bwd_q_item<E>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale, scale_log2,
                   qstat);
@@ -626,7 +651,8 @@ __global__ __launch_bounds__(256) void bwd_gqa_sum_kernel(const uint16_t* __rest
                                                           const uint16_t* __restrict__ dv_part,
                                                           uint16_t* __restrict__ dk,
                                                           uint16_t* __restrict__ dv, long n8,
-                                                          int hq, int hkv) {
+                                                          int hq, int hkv,
+                                                          const uint32_t* __restrict__ flags) {
   long i = (long)blockIdx.x * 256 + threadIdx.x;
   const uint16_t* src = dk_part;
   uint16_t* dst = dk;
@@ -641,6 +667,7 @@ __global__ __launch_bounds__(256) void bwd_gqa_sum_kernel(const uint16_t* __rest
   const int c = (int)(i & 15);
   const long token = r / hkv;
   const int kvh = (int)(r - token * hkv);
+  if (flags != nullptr && flags[token] != 0) return;  // a group item wrote this row itself
   const int g = hq / hkv;
   const uint16_t* p = src + (token * hq + (long)kvh * g) * kHeadDim + 8 * c;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -667,7 +694,8 @@ static hipError_t launch_bwd_main_t(const BwdArgs& a) {
                      (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.out, (const uint16_t*)a.dout, a.hq,
                      a.hkv, a.lse, (uint16_t*)a.dq, (uint16_t*)a.dk_part, (uint16_t*)a.dv_part,
-                     (int)a.n_tokens, a.scale, a.scale * kLog2e);
+                     (int)a.n_tokens, a.scale, a.scale * kLog2e, (uint16_t*)a.dk,
+                     (uint16_t*)a.dv, a.flags);
   return hipGetLastError();
 }
 
@@ -678,7 +706,7 @@ static hipError_t launch_bwd_finish_t(const BwdArgs& a) {
   if (n8 == 0) return hipSuccess;
   hipLaunchKernelGGL(bwd_gqa_sum_kernel<E>, dim3((unsigned)((2 * n8 + 255) / 256)), dim3(256), 0,
                      a.stream, (const uint16_t*)a.dk_part, (const uint16_t*)a.dv_part,
-                     (uint16_t*)a.dk, (uint16_t*)a.dv, n8, a.hq, a.hkv);
+                     (uint16_t*)a.dk, (uint16_t*)a.dv, n8, a.hq, a.hkv, a.flags);
   return hipGetLastError();
 }
 

@@ -45,7 +45,10 @@ constexpr int64_t kQItemCost = va::kPlanQItemCost;
 
 bool is_plan_kind(int32_t kind) {
   return kind == VA_PLAN_FWD || kind == VA_PLAN_BWD || kind == VA_PLAN_BWD_HEADS ||
-         kind == VA_PLAN_BWD_PAIRS;
+         kind == VA_PLAN_BWD_PAIRS || kind == VA_PLAN_BWD_GROUPS || kind == VA_PLAN_BWD_GROUPS_ALL;
+}
+bool is_group_kind(int32_t kind) {
+  return kind == VA_PLAN_BWD_GROUPS || kind == VA_PLAN_BWD_GROUPS_ALL;
 }
 int32_t item_head(int32_t d) { return d & (va::kItemPairBit - 1); }
 
@@ -54,6 +57,22 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
   std::vector<Item> items;
   const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
   const int32_t group = hq / hkv, rows = pairs ? (group + 1) / 2 : group;
+  // Group plans: the largest group-item work that keeps the plan about as long as its VA_PLAN_BWD
+  // form: that list's longest item, or its work per CU when that is more (measured at configs
+  // 3-5: half the work per CU left config 4 7% slower, all key tiles grouped config 3 50%).
+  int64_t group_cap = -1;
+  if (is_group_kind(kind) && group >= 2) {
+    if (kind == VA_PLAN_BWD_GROUPS_ALL) {
+      group_cap = INT64_MAX;
+    } else {
+      int64_t longest = 0, total = 0;
+      for (const Item& x : make_items(cu, n_docs, hq, hkv, VA_PLAN_BWD)) {
+        longest = std::max(longest, x.work);
+        total += x.work;
+      }
+      group_cap = std::max(longest, total / va::kPlanCus);
+    }
+  }
   for (int32_t i = 0; i < n_docs; ++i) {
     const int32_t s = cu[i], e = cu[i + 1];
     if (e <= s) continue;
@@ -72,8 +91,15 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
       // 384 queries (18.7 us) ties with a q item over 512 keys (17.3 us), and the XCD layout
       // below deals the heavier ones to the same XCDs in every block.
       // A pair item's halves each take one head over every step: twice a per-head item's steps.
+      // A group item's halves take the G heads' steps in sequence, two per step pair.
       for (int32_t k0 = s; k0 < e; k0 += va::kBwdBlockN) {
         const int64_t steps = ((int64_t)e - k0 + va::kBwdBlockQ - 1) / va::kBwdBlockQ;
+        const int64_t group_work = (group * steps + 1) / 2 * 32 + kKvItemCost;
+        if (group_work <= group_cap) {
+          for (int32_t g = 0; g < hkv; ++g)
+            items.push_back({k0, e, s, va::kItemGroupBit | (g * group), group_work});
+          continue;
+        }
         for (int32_t g = 0; g < hkv; ++g)
           for (int32_t r = 0; r < rows; ++r) {
             const bool pair = pairs && 2 * r + 1 < group;
@@ -136,6 +162,7 @@ std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
 }
 
 int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind) {
+  if (is_group_kind(kind)) return (int64_t)make_items(cu, n_docs, hq, hkv, kind).size();
   int64_t n = 0;
   const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
   const int64_t kv_per_tile = pairs ? (int64_t)hkv * ((hq / hkv + 1) / 2) : hq;  // per kind
@@ -228,7 +255,9 @@ extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_
   const hipError_t e = va::launch_plan_device(
       cu_seqlens_device, nullptr, n_docs, (int)n_tokens, hq, hkv, fwd ? items_device : nullptr,
       capacity, fwd ? nullptr : items_device, capacity,
-      !fwd && va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, kind), nullptr, (hipStream_t)stream);
+      !fwd && va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, kind),
+      kind == VA_PLAN_BWD_GROUPS ? 1 : (kind == VA_PLAN_BWD_GROUPS_ALL ? 2 : 0), nullptr,
+      (hipStream_t)stream);
   if (e != hipSuccess) return va::fail((int)e, "va_plan_build_device launch: %s", hipGetErrorString(e));
   return VA_OK;
 }
@@ -254,7 +283,7 @@ extern "C" int va_plan_build_device_lengths(const int64_t* lengths_device, int32
   const hipError_t e = va::launch_plan_device(
       nullptr, lengths_device, n_docs, (int)n_tokens, hq, hkv, fwd_items_device, fwd_capacity,
       bwd_items_device, bwd_capacity, va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, VA_PLAN_BWD),
-      cu_seqlens_out, (hipStream_t)stream);
+      0, cu_seqlens_out, (hipStream_t)stream);
   if (e != hipSuccess)
     return va::fail((int)e, "va_plan_build_device_lengths launch: %s", hipGetErrorString(e));
   return VA_OK;

@@ -66,7 +66,8 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
                                                   int n_tokens, int hq, int hkv,
                                                   int4* __restrict__ fwd_items, long fwd_capacity,
                                                   int4* __restrict__ bwd_items, long bwd_capacity,
-                                                  int bwd_pairs, int32_t* __restrict__ cu_out) {
+                                                  int bwd_pairs, int bwd_groups,
+                                                  int32_t* __restrict__ cu_out) {
   __shared__ int s_bound[kPlanMaxDocs + 1];  // clamped, non-decreasing document bounds
   __shared__ int s_tbase[kPlanMaxDocs + 1];  // exclusive prefix of the per-document tile counts
   __shared__ int s_cnt[kBuckets];
@@ -167,20 +168,65 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
     doc = lo;
     t = ct - s_tbase[lo];
   };
-  // The host planner's work measures (plan.cpp), in buckets of 8.
-  auto bucket = [&](int doc, int t, int is_q) {
+  // The host planner's work measures (plan.cpp): of a per-head item (w1) and of a pair item (w2)
+  // of the candidate, of a kv candidate's group item (wg).
+  auto works = [&](int doc, int t, int is_q, long& w1, long& w2, long& wg) {
     const long s = s_bound[doc], e = s_bound[doc + 1];
-    long work;
     if (kind == VA_PLAN_FWD) {
-      work = min(s + (long)(t + 1) * kTile, e) - s;
+      w1 = w2 = wg = min(s + (long)(t + 1) * kTile, e) - s;
     } else if (!is_q) {
       const long steps = (e - (s + (long)t * kTile) + kBwdBlockQ - 1) / kBwdBlockQ;
-      work = (pairs ? steps : (steps + 1) / 2) * 32 + kPlanKvItemCost;
+      w1 = (steps + 1) / 2 * 32 + kPlanKvItemCost;
+      w2 = steps * 32 + kPlanKvItemCost;
+      wg = (group * steps + 1) / 2 * 32 + kPlanKvItemCost;
     } else {
       const long kv_end = min(s + (long)(t + 1) * kTile, e);
       const long tiles = (kv_end - s + kBwdTileK - 1) / kBwdTileK;
-      work = (tiles + 1) / 2 * (pairs ? 48 : 24) + kPlanQItemCost;
+      w1 = (tiles + 1) / 2 * 24 + kPlanQItemCost;
+      w2 = (tiles + 1) / 2 * 48 + kPlanQItemCost;
+      wg = LONG_MAX;
     }
+  };
+  // Group plans: a kv candidate becomes one group item per GQA group when that item's work is at
+  // most the longest item of the list without groups, or that list's work per CU (plan.cpp).
+  const bool groups = kind == VA_PLAN_BWD && bwd_groups != 0 && group >= 2;
+  long long group_cap = -1;
+  if (groups) {
+    if (bwd_groups == 2) {
+      group_cap = LLONG_MAX;
+    } else {
+      long long longest = 0, total = 0;
+      for (int c = tid; c < n_cand; c += PT) {
+        int doc, t, is_q;
+        decode(c, doc, t, is_q);
+        long w1, w2, wg;
+        works(doc, t, is_q, w1, w2, wg);
+        long per = 0;  // the candidate's items over one GQA group
+        for (int r = 0; r < (pairs ? (group + 1) / 2 : group); ++r)
+          per += (pairs && 2 * r + 1 < group) ? w2 : w1;
+        longest = max(longest, (long long)(pairs ? w2 : w1));
+        total += per * hkv;
+      }
+      block_scan<kScanMax>(longest, s_scan);
+      longest = s_scan[PT - 1];
+      __syncthreads();
+      block_scan<kScanSum>(total, s_scan);
+      total = s_scan[PT - 1];
+      __syncthreads();
+      group_cap = max(longest, total / kPlanCus);
+    }
+  }
+  auto is_group = [&](int doc, int t, int is_q) {
+    if (!groups || is_q) return false;
+    long w1, w2, wg;
+    works(doc, t, is_q, w1, w2, wg);
+    return wg <= group_cap;
+  };
+  // The work measure in buckets of 8.
+  auto bucket = [&](int doc, int t, int is_q) {
+    long w1, w2, wg;
+    works(doc, t, is_q, w1, w2, wg);
+    const long work = is_group(doc, t, is_q) ? wg : (pairs ? w2 : w1);
     const long b = work >> 3;
     return (int)(b >= kBuckets ? kBuckets - 1 : b);
   };
@@ -213,13 +259,14 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   // in column j % 8 of block j / 8, which spans 8 G slots (fewer columns in the last block);
   // head r of the group goes to row r. In a pair plan a combo's row r < ceil(G / 2) holds the
   // item of heads 2 r, 2 r + 1 (the last head of an odd group alone) and its other rows stay
-  // empty items.
+  // empty items; a group candidate's combo holds its group item in row 0, empty items below.
   const long n_combos = (long)n_cand * hkv;
   for (int c = tid; c < n_cand; c += PT) {
     int doc, t, is_q;
     decode(c, doc, t, is_q);
     const long pos = atomicAdd(&s_cnt[bucket(doc, t, is_q)], 1);
     const int s = s_bound[doc], e = s_bound[doc + 1];
+    const bool grouped = is_group(doc, t, is_q);
     for (int g = 0; g < hkv; ++g) {
       const long combo = pos * hkv + g;
       const long blk = combo / kXcds, col = combo % kXcds;
@@ -227,7 +274,9 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       for (int r = 0; r < group; ++r) {
         const long slot = blk * kXcds * group + r * ncols + col;
         int4 item = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
-        if (pairs) {
+        if (grouped) {
+          item = r == 0 ? int4{s + t * kTile, e, s, kItemGroupBit | (g * group)} : int4{0, 0, 0, 0};
+        } else if (pairs) {
           const int h2 = 2 * r;
           item = h2 < group ? int4{s + t * kTile, e, s,
                                    (is_q << 24) | (h2 + 1 < group ? kItemPairBit : 0) |
@@ -246,10 +295,10 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
                               int32_t* bwd_items, long bwd_capacity, bool bwd_pairs,
-                              int32_t* cu_out, hipStream_t stream) {
+                              int bwd_groups, int32_t* cu_out, hipStream_t stream) {
   hipLaunchKernelGGL(plan_kernel, dim3(2), dim3(PT), 0, stream, cu, lengths, n_docs, n_tokens, hq,
                      hkv, (int4*)fwd_items, fwd_capacity, (int4*)bwd_items, bwd_capacity,
-                     (int)bwd_pairs, cu_out);
+                     (int)bwd_pairs, bwd_groups, cu_out);
   return hipGetLastError();
 }
 

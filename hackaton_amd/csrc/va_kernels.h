@@ -23,10 +23,15 @@ constexpr int kPlanMaxDocs = 8192;  // documents a device-built plan takes (LDS-
 // wave per step pair: 32 per kv step pair, 24 per q tile pair (from in-graph item durations).
 constexpr int kPlanKvItemCost = 39;
 constexpr int kPlanQItemCost = 30;
+constexpr int kPlanCus = 256;  // compute units the plans balance work over (MI355X)
 // VA_PLAN_BWD takes two query heads per item (pair items, Hq > Hkv) once the per-head list
 // would be this long (2 (ceil(N / 128) + n_docs) Hq items: every CU then holds several).
 constexpr int kBwdPairMinItems = 1024;
-constexpr int kItemPairBit = 1 << 20;  // item word: kind << 24 | pair << 20 | head
+constexpr int kItemPairBit = 1 << 20;  // item word: kind << 24 | group << 21 | pair << 20 | head
+// A kv item over every query head of a GQA group (group items): its halves walk the G heads'
+// steps in sequence and it writes dK/dV of the key tile at Hkv width, so the tile needs no
+// per-head partials and no GQA sum.
+constexpr int kItemGroupBit = 1 << 21;
 // Whether a backward plan of `kind` for these host-known sizes has pair items.
 inline bool bwd_plan_pairs(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t hkv, int kind) {
   if (kind == 2 || hkv <= 0 || hq / hkv < 2) return false;  // VA_PLAN_BWD_HEADS, or no group
@@ -68,6 +73,8 @@ struct BwdArgs {
   void* dv_part;
   void* dk;         // (n_tokens, hkv, 128) GQA sums, or null to keep the per-head partials
   void* dv;
+  uint32_t* flags;  // (n_tokens) 1 where a group item wrote dK/dV itself (the GQA sum skips the
+                    // row), 0 where per-head partials hold it; null when Hq == Hkv
   hipStream_t stream;
 };
 
@@ -109,6 +116,7 @@ hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, co
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
                               int32_t* bwd_items, long bwd_capacity, bool bwd_pairs,
+                              int bwd_groups,
                               int32_t* cu_out, hipStream_t stream);
 
 }  // namespace va

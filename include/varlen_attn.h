@@ -51,7 +51,8 @@ enum {
 };
 
 enum { VA_F16 = 0, VA_BF16 = 1, VA_F32 = 2 };
-enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1, VA_PLAN_BWD_HEADS = 2, VA_PLAN_BWD_PAIRS = 3 };
+enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1, VA_PLAN_BWD_HEADS = 2, VA_PLAN_BWD_PAIRS = 3,
+       VA_PLAN_BWD_GROUPS = 4, VA_PLAN_BWD_GROUPS_ALL = 5 };
 enum { VA_BWD_PAIR_MIN_ITEMS = 1024 };
 enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
 enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2 };
@@ -69,8 +70,16 @@ int32_t va_head_dim(void);
  * items, heads otherwise) over the documents of cu_seqlens, longest first. The items of one tile
  * and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the heads
  * sharing K/V run on one XCD and share its L2. Fully masked causal tiles and cross-document tiles
- * never appear. Every plan kind gives the same outputs up to rounding (a pair item sums a head's
- * steps or tiles in one sequence instead of two halves); each is deterministic.
+ * never appear. VA_PLAN_BWD_GROUPS is VA_PLAN_BWD with GQA group items where they do not lengthen
+ * the plan: a key tile whose dK/dV item over all G query heads of a group does no more work than
+ * the longest item of the VA_PLAN_BWD list, or than the list's work per CU (256 CUs), gets one
+ * such item per GQA group instead of its per-head or pair items; it writes that tile's dK/dV
+ * itself (Hkv width), with no per-head partials and nothing for the GQA sum to do there.
+ * VA_PLAN_BWD_GROUPS_ALL makes every key tile a group tile. Group plans need dk/dv in va_bwd
+ * (group items have no per-head partials to leave behind) and Hq > Hkv, and are built on the
+ * host only. Every plan kind gives the same outputs up to rounding (a pair item sums a head's
+ * steps or tiles in one sequence instead of two halves, a group item the G heads' in one); each
+ * is deterministic.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
 int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                  int64_t* n_items);
@@ -127,8 +136,10 @@ int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
  * Deterministic and atomic-free. dq (N, Hq, 128) is always written. dk/dv (N, Hkv, 128) are the
  * sums over each GQA group of per-query-head partials (N, Hq, 128, element type) that live in the
  * workspace at the offsets va_bwd_workspace_layout reports; with dk = dv = NULL the partials are
- * the result (a rotary backward can sum them, as the reference sums its expanded copies). With
- * Hq == Hkv and dk/dv given, no workspace is used. The caller's O and lse come from va_fwd;
+ * the result (a rotary backward can sum them, as the reference sums its expanded copies; the plan
+ * must then have no group items). The workspace ends with one uint32 flag per row, past the two
+ * partial arrays, that marks the rows whose dK/dV a group item wrote. With Hq == Hkv and dk/dv
+ * given, no workspace is used. The caller's O and lse come from va_fwd;
  * rowsum(dO * O) is computed inside.
  * Replaces: solution/attention.py:230-232 (aten::_efficient_attention_backward) and the GQA
  * reduction of dk/dv at solution/attention.py:113-134. */
@@ -142,8 +153,8 @@ int va_bwd(const void* dout, const void* q, const void* k, const void* v, const 
 /* The same backward for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. Same inputs and outputs as va_bwd, no workspace: the dK/dV partials live in a static
- * device array of the library (va_bwd_noalloc_max_bytes() = 64 MiB per GPU, held until the
- * process ends), so total_tokens * Hq must not exceed 131072 at head_dim 128 (VA_ECAPACITY
+ * device array of the library (va_bwd_noalloc_max_bytes() = 65 MiB per GPU, held until the
+ * process ends: partials and row flags), so total_tokens * Hq must not exceed 131072 at head_dim 128 (VA_ECAPACITY
  * otherwise, before any launch); dk and dv must be given. Calls nothing that allocates. Calls
  * that overlap on one GPU (two streams or two threads) race on the shared array. */
 int64_t va_bwd_noalloc_max_bytes(void);

@@ -54,7 +54,7 @@ def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
     check_xcd_order(items, hq, hkv, lambda q0, e, s, w: min(q0 + 128, e) - s)
 
 
-HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | pair << 20 | head
+HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | group << 21 | pair << 20 | head
 
 
 def check_xcd_order(items, hq, hkv, work_of, per_combo=None):
@@ -94,11 +94,14 @@ def test_backward_plan_deals_every_xcd_the_same_items():
     assert all(m == mixes[0] for m in mixes)
 
 
-def bwd_work(a, e, s, w):
+def bwd_work(a, e, s, w, g=1):
     """The planners' measure: MFMAs per wave per iteration + item cost (a pair item's halves each
-    take every step of one head; a per-head item's halves take alternate steps)."""
+    take every step of one head; a per-head item's halves take alternate steps; a group item's
+    halves alternate over the G heads' steps)."""
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
+        if (w >> 21) & 1:
+            return (g * steps + 1) // 2 * 32 + 39
         return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
     return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * (48 if (w >> 20) & 1 else 24) + 30
 
@@ -148,6 +151,56 @@ def test_backward_plan_covers_every_key_and_query_tile_once(lengths, hq, hkv, ki
         check_xcd_order(items, hq, hkv, bwd_work, per_combo)
     else:
         check_xcd_order(items, hq, hkv, bwd_work)
+
+
+@pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1], [257, 3], [1000, 24, 300],
+                                     [180] * 45, [1740, 400, 90]])
+@pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (12, 12), (4, 1)])
+@pytest.mark.parametrize("kind", [_lib.VA_PLAN_BWD_GROUPS, _lib.VA_PLAN_BWD_GROUPS_ALL])
+def test_group_plan_covers_every_tile_once(lengths, hq, hkv, kind):
+    """Group plans: every key tile is covered either by one group item per GQA group (first head
+    of the group, bit 21) or by the VA_PLAN_BWD items of that tile for every head; every query
+    tile by the VA_PLAN_BWD q items. VA_PLAN_BWD_GROUPS groups exactly the key tiles whose group
+    item does no more work than the VA_PLAN_BWD list's longest item or its work per CU (256);
+    VA_PLAN_BWD_GROUPS_ALL all of them; with Hq == Hkv both are VA_PLAN_BWD."""
+    g = hq // hkv
+    cu, items = plan(lengths, hq, hkv, kind)
+    _, base = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
+    if g == 1:
+        assert np.array_equal(items, base)
+        return
+    base_works = [bwd_work(*x) for x in base.tolist()]
+    cap = max(max(base_works), sum(base_works) // 256)
+    group_tiles = set()
+    for a, e, s, w in items.tolist():
+        if (w >> 21) & 1:
+            assert w >> 24 == 0 and (w & HEAD_MASK) % g == 0 and not (w >> 20) & 1
+            group_tiles.add((a, e, s))
+    for a, e, s in {(a, e, s) for a, e, s, w in items.tolist() if w >> 24 == 0}:
+        grouped = kind == _lib.VA_PLAN_BWD_GROUPS_ALL or bwd_work(a, e, s, 1 << 21, g) <= cap
+        assert ((a, e, s) in group_tiles) == grouped, (a, e, s)
+    kept = [tuple(x) for x in base.tolist() if x[3] >> 24 == 1 or tuple(x[:3]) not in group_tiles]
+    grp = [tuple(x) for x in items.tolist() if (x[3] >> 21) & 1]
+    assert sorted(kept + grp) == sorted(map(tuple, items.tolist()))
+    assert sorted(grp) == sorted((a, e, s, (1 << 21) | (k * g)) for a, e, s in group_tiles
+                                 for k in range(hkv))
+    bound = 2 * (-(-sum(lengths) // 128) + len(lengths)) * hq
+    pairs = bound >= _lib.VA_BWD_PAIR_MIN_ITEMS
+
+    def per_combo(key):  # a group item alone; otherwise as in the VA_PLAN_BWD list
+        a, e, s, item_kind, _grp, work = key
+        if item_kind == 0 and (a, e, s) in group_tiles:
+            return 1
+        if not pairs:
+            return g
+        single = bwd_work(a, e, s, item_kind << 24)
+        pair = bwd_work(a, e, s, (item_kind << 24) | (1 << 20))
+        if g % 2 == 0:
+            return g // 2
+        if pair == single:
+            return (g + 1) // 2
+        return 1 if work == single else g // 2
+    check_xcd_order(items, hq, hkv, lambda a, e, s, w: bwd_work(a, e, s, w, g), per_combo)
 
 
 @pytest.mark.parametrize("lengths,pairs", [([512] * 4, False), ([64, 37, 50, 12], False),
@@ -210,7 +263,7 @@ def test_attention_entry_points_validate_before_launching():
     nbytes = ctypes.c_int64()
     assert lib.va_bwd_workspace_layout(2048, 12, 2, 128, offs, ctypes.byref(nbytes)) == 0
     assert list(offs) == [0, 2048 * 12 * 256]
-    assert nbytes.value == 2 * 2048 * 12 * 256
+    assert nbytes.value == 2 * 2048 * 12 * 256 + 2048 * 4  # partials, then one flag per row
     rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, fake,
                     None, None, fake, nbytes.value - 1, None)
     assert rc == _lib.VA_ECAPACITY
@@ -241,7 +294,8 @@ def test_product_path_refuses_cpu_tensors():
 @pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1, 1, 1], [129, 0, 300],
                                      [4096, 17], [127, 128, 129]])
 @pytest.mark.parametrize("kind", [_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD, _lib.VA_PLAN_BWD_HEADS,
-                                  _lib.VA_PLAN_BWD_PAIRS])
+                                  _lib.VA_PLAN_BWD_PAIRS, _lib.VA_PLAN_BWD_GROUPS,
+                                  _lib.VA_PLAN_BWD_GROUPS_ALL])
 def test_device_plan_capacity_bounds_the_host_plan(lengths, kind):
     """va_plan_capacity, from host-known sizes only, is never below the real item count."""
     hq = 12

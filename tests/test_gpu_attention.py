@@ -132,6 +132,9 @@ class _Plan:
         self.bwd_items, self.n_bwd = bwd, bwd.shape[0]
         self.total = total
 
+    def partial_bwd(self):
+        return self.bwd_items, self.n_bwd
+
 
 @pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
 def test_pair_backward_matches_oracle(lengths, hq, hkv, dtype):
@@ -148,6 +151,37 @@ def test_pair_backward_matches_oracle(lengths, hq, hkv, dtype):
     cu = np.concatenate([[0], np.cumsum([x for x in lengths if x])]).astype(np.int32)
     pair_items = torch.from_numpy(att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_BWD_PAIRS))
     plan = _Plan(base.fwd_items[: base.n_fwd], pair_items.to(dev), n)
+    qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
+    out, lse = att.attention_forward(qd, kd, vd, plan, SCALE)
+    runs = [att.attention_backward(dod, qd, kd, vd, out, lse, plan, SCALE) for _ in range(2)]
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    ref = oracle(q, k, v, do, lengths)
+    check_all(out.cpu(), tuple(t.cpu() for t in runs[0]), ref, dtype, n, hq)
+
+
+@pytest.mark.parametrize("kind", ["all", "auto"])
+@pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
+def test_group_backward_matches_oracle(lengths, hq, hkv, dtype, kind):
+    """Backward plans with GQA group items (one kv item over all G query heads of a group, writing
+    dK/dV at Hkv width): every key tile grouped (VA_PLAN_BWD_GROUPS_ALL), and the planner's mix
+    of group tiles and per-head or pair tiles (VA_PLAN_BWD_GROUPS, where the GQA sum must skip
+    the group tiles' rows). dQ/dK/dV against the oracle, and bitwise equal over two runs."""
+    qk = 3.0 if dtype == "peaky" else 1.0
+    dtype = torch.bfloat16 if dtype == "peaky" else dtype
+    banner("group backward", kind, lengths, hq, hkv, dtype, qk)
+    q, k, v, do = wl.make_inputs(lengths, hq, hkv, dtype, seed=sum(lengths) + 4, qk_scale=qk)
+    n = sum(lengths)
+    dev = torch.device("cuda")
+    base = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
+    cu = np.concatenate([[0], np.cumsum([x for x in lengths if x])]).astype(np.int32)
+    code = att._lib.VA_PLAN_BWD_GROUPS_ALL if kind == "all" else att._lib.VA_PLAN_BWD_GROUPS
+    items = att.build_plan_host(cu, hq, hkv, code)
+    if hq > hkv and kind == "all":
+        kv = items[(items[:, 3] >> 24) == 0]
+        assert len(kv) and ((kv[:, 3] >> 21) & 1).all()
+    plan = _Plan(base.fwd_items[: base.n_fwd], torch.from_numpy(items).to(dev), n)
     qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
     out, lse = att.attention_forward(qd, kd, vd, plan, SCALE)
     runs = [att.attention_backward(dod, qd, kd, vd, out, lse, plan, SCALE) for _ in range(2)]
@@ -444,13 +478,16 @@ def test_packed_attention_matches_oracle(dtype):
 HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | pair << 20 | head
 
 
-def plan_work(kind, a, e, s, w):
+def plan_work(kind, a, e, s, w, g=1):
     """The planners' work measure of an item: keys visited (forward); MFMAs per wave per
-    iteration plus the item's fixed cost (backward; a pair item's halves take every step)."""
+    iteration plus the item's fixed cost (backward; a pair item's halves take every step, a
+    group item's the G heads' steps)."""
     if kind == 0:
         return min(a + 128, e) - s
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
+        if (w >> 21) & 1:
+            return (g * steps + 1) // 2 * 32 + 39
         return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
     return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * (48 if (w >> 20) & 1 else 24) + 30
 
@@ -458,7 +495,7 @@ def plan_work(kind, a, e, s, w):
 def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
     """The items of one (tile, kind, GQA group) sit a constant stride apart, at most 8 (one XCD),
     and the groups come longest first by the work measure in buckets of 8. Empty items (the
-    rows a pair plan leaves free) are skipped."""
+    rows a pair plan or a group item leaves free) are skipped; a group item is its combo alone."""
     g = hq // hkv
     combos = {}
     for pos, (a, e, s, w) in enumerate(items.tolist()):
@@ -468,11 +505,12 @@ def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
     firsts = []
     for key, entries in combos.items():
         pos = [p for p, _ in entries]
-        assert len(pos) == (g if not pairs else (g + 1) // 2), key
+        grouped = (entries[0][1] >> 21) & 1
+        assert len(pos) == (1 if grouped else (g if not pairs else (g + 1) // 2)), key
         steps = {b - a for a, b in zip(pos, pos[1:])}
         assert len(steps) <= 1 and all(0 < x <= 8 for x in steps), (key, pos)
-        w0 = (key[3] << 24) | ((1 << 20) if pairs and g > 1 else 0)
-        firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], w0) // 8))
+        w0 = (key[3] << 24) | ((1 << 20) if pairs and g > 1 and not grouped else 0) | (grouped << 21)
+        firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], w0, g) // 8))
     work = [w for _, w in sorted(firsts)]
     assert work == sorted(work, reverse=True)
 
@@ -492,13 +530,21 @@ def test_device_plan_matches_host_plan(lengths):
     torch.cuda.synchronize()
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     assert dplan.cu.cpu().numpy().tolist() == cu.tolist()
-    for kind, items, count in ((0, dplan.fwd_items, dplan.n_fwd), (1, dplan.bwd_items, dplan.n_bwd)):
+    groups = att._lib.VA_PLAN_BWD_GROUPS
+    part_items, part_n = dplan.partial_bwd()
+    for kind, items, count in ((0, dplan.fwd_items, dplan.n_fwd), (1, part_items, part_n),
+                               (groups, dplan.bwd_items, dplan.n_bwd)):
         host = att.build_plan_host(cu, hq, hkv, kind)
         got = items.cpu().numpy()[:count]
-        real, empty = got[: len(host)], got[len(host):]
-        assert sorted(map(tuple, real.tolist())) == sorted(map(tuple, host.tolist()))
-        assert not empty.any()
-        check_device_xcd_layout(real, kind, hq, hkv)
+        if kind == groups:  # group combos leave their other rows empty
+            real = [tuple(x) for x in got.tolist() if any(x)]
+            assert sorted(real) == sorted(map(tuple, host.tolist()))
+            check_device_xcd_layout(got, kind, hq, hkv)
+        else:
+            real, empty = got[: len(host)], got[len(host):]
+            assert sorted(map(tuple, real.tolist())) == sorted(map(tuple, host.tolist()))
+            assert not empty.any()
+            check_device_xcd_layout(real, kind, hq, hkv)
         again = torch.empty_like(items)
         att.check(att.lib().va_plan_build_device(dplan.cu.data_ptr(), len(lengths), n, hq, hkv,
                                                  kind, again.data_ptr(), count, att._stream()),
@@ -519,6 +565,17 @@ def test_device_plan_matches_host_plan(lengths):
     real = [tuple(x) for x in got.tolist() if any(x)]
     assert sorted(real) == sorted(map(tuple, host.tolist()))
     check_device_xcd_layout(got, 1, hq, hkv, pairs=True)
+    # every key tile as group items, from the device cu_seqlens
+    all_items = torch.empty_like(dplan.bwd_items)
+    att.check(att.lib().va_plan_build_device(dplan.cu.data_ptr(), len(lengths), n, hq, hkv,
+                                             att._lib.VA_PLAN_BWD_GROUPS_ALL,
+                                             all_items.data_ptr(), count, att._stream()),
+              "va_plan_build_device")
+    torch.cuda.synchronize()
+    got = all_items.cpu().numpy()[:count]
+    host = att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_BWD_GROUPS_ALL)
+    assert sorted(tuple(x) for x in got.tolist() if any(x)) == sorted(map(tuple, host.tolist()))
+    check_device_xcd_layout(got, 1, hq, hkv)
 
 
 def test_device_lengths_plan_is_rebuilt_inside_a_captured_graph():
