@@ -540,7 +540,11 @@ __global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
   __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
-  auto visible = [&](int t) { return doc_start + t * BN <= wq0_u + 31; };
+  // A strip past the document's end (the last item of a document whose length is not a multiple
+  // of 128) has no query to compute: its wave only copies and meets the barriers, and leaves its
+  // SIMD to the other work-group's wave.
+  const bool strip_live = wq0_u < doc_end;
+  auto visible = [&](int t) { return strip_live && doc_start + t * BN <= wq0_u + 31; };
   for (int t = 0; t < n_tiles; ++t) {
     const int stage = t & 1;
     // The next tile's copies go out after this tile's S^T MFMAs (the wave waits for S anyway).
