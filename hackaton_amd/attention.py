@@ -108,9 +108,11 @@ class Plan:
         self.fwd_items = torch.from_numpy(host_fwd).to(device)
         self.bwd_items = torch.from_numpy(host_bwd).to(device)
         self._part = None if hq > hkv else (self.bwd_items, self.n_bwd)
-        # whether the backward needs its GQA sum: not when group items cover every key tile
+        # whether the backward needs its GQA sum: not when every key tile's group items take the
+        # whole GQA group (item word: group bit 21, heads - 1 in bits 12-19)
         kv = host_bwd[(host_bwd[:, 3] >> 24) == 0]
-        self.bwd_finish = hq > hkv and not bool(((kv[:, 3] >> 21) & 1).all())
+        whole = (((kv[:, 3] >> 21) & 1) == 1) & ((((kv[:, 3] >> 12) & 0xFF) + 1) == hq // hkv)
+        self.bwd_finish = hq > hkv and not bool(whole.all())
 
     def partial_bwd(self):
         """(items, n) of the backward list without group items (built on first use)."""

@@ -46,7 +46,7 @@ constexpr int Q_HALFS = 2 * Q_PAIR;
 constexpr int HALFS = KV_HALFS > Q_HALFS ? KV_HALFS : Q_HALFS;
 static_assert(BK == kBwdBlockN && QB == kBwdBlockM && BQ == kBwdBlockQ, "plan tile sizes");
 constexpr int kKindKV = 0, kKindQ = 1;
-constexpr int kHeadMask = (1 << 20) - 1;  // item word: kind << 24 | pair << 20 | head
+constexpr int kHeadMask = kItemHeadMask;  // item word: see kItemGroupBit
 // Transposed operand reads (Q^T, dO^T, K^T): the second 16-lane group of a wave reads 64 columns
 // (d) over the first (TRG), so that the 32 lanes one LDS cycle serves hit 64 distinct banks of
 // the 272-byte rows; 16 columns over, as the accumulator layout would suggest, they overlapped on
@@ -79,7 +79,9 @@ __device__ __forceinline__ void bwd_kv_item(
   using namespace bwd;
   const int k0 = it.x, doc_end = it.y, h = it.w & kHeadMask;
   const bool pair = (it.w >> 20) & 1;
-  const bool all_heads = (it.w >> 21) & 1;  // group item: heads h .. h + G - 1 in sequence
+  // Group items walk heads h .. h + S - 1 in sequence (S = G: the whole GQA group).
+  const bool grouped = (it.w >> 21) & 1;
+  const int S = grouped ? ((it.w >> kItemHeadsShift) & 0xff) + 1 : 1;
   const int G = hq / hkv;
   const int kvh = h / G;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
@@ -104,7 +106,7 @@ __device__ __forceinline__ void bwd_kv_item(
   // Units of work: (head, step) in head-major order, over one head or (group items) the G heads
   // of the group. Iterations of the step loop: a pair of units (the halves take alternate units),
   // or one step of each head of a pair item.
-  const int n_units = (all_heads ? G : 1) * n_steps;
+  const int n_units = S * n_steps;
   const int n_iter = pair ? n_steps : (n_units + 1) / 2;
   auto unit_of = [&](int p, int j) { return min(2 * p + j, n_units - 1); };  // clamped: loads
   auto step_of = [&](int p, int j) { return pair ? p : unit_of(p, j) % n_steps; };
@@ -319,10 +321,10 @@ __device__ __forceinline__ void bwd_kv_item(
     store_rows32<16>(reinterpret_cast<lds_u16*>(&xs[slot(half, 0, 0) - lane]), w, lane,
                     [&](int r) { return part + ((long)(kw0 + r) * rs + hd) * D; }, doc_end - kw0);
   };
-  // The GQA sum reads which rows a group item finished (1) and which per-head partials hold (0):
-  // every key row belongs to one tile, whose group items or first head's items write its flags.
-  if (flags != nullptr && (all_heads || h % G == 0) && tid < BK && k0 + tid < doc_end)
-    flags[k0 + tid] = all_heads ? 1u : 0u;
+  // The GQA sum reads how many heads each partial of a row sums (S; G: a group item wrote the
+  // row's dK/dV itself): every key row belongs to one tile, whose items of the GQA group's first
+  // head write its flag.
+  if (flags != nullptr && h % G == 0 && tid < BK && k0 + tid < doc_end) flags[k0 + tid] = S;
   if (pair) {
     // Each half holds the whole dK/dV of its head: both go out through this wave's own row tile
     // (the LDS stages are free after the loop's last barrier), dK scaled.
@@ -355,7 +357,7 @@ __device__ __forceinline__ void bwd_kv_item(
     store(dvacc, 1.f, dv_part);
     return;
   }
-  if (all_heads) {
+  if (S == G) {
     if (half) finish(dvacc, dkacc, 1.f, dv_out, hkv, kvh);
     else finish(dkacc, dvacc, scale, dk_out, hkv, kvh);
   } else {
@@ -635,12 +637,15 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
   // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
   const int kind = it.w >> 24, h = it.w & bwd::kHeadMask, shape = (it.w >> 20) & 15;
   // Pair items (shape 1) take heads h, h + 1 of one GQA group; group items (shape 2, kv only)
-  // every head of the group that starts at h, and need the Hkv-wide outputs.
-  const int G = hq / hkv;
+  // heads h .. h + S - 1 (S >= 2 dividing G, h a multiple of S), and with S = G need the Hkv-wide
+  // outputs.
+  const int G = hq / hkv, S = ((it.w >> kItemHeadsShift) & 0xff) + 1;
   if (it.x >= it.y || it.z < 0 || it.x < it.z || it.y > n_tokens || h >= hq ||
       (kind != bwd::kKindKV && kind != bwd::kKindQ) || shape > 2 ||
+      (shape < 2 && S != 1) ||
       (shape == 1 && (h + 1 >= hq || h / G != (h + 1) / G)) ||
-      (shape == 2 && (kind != bwd::kKindKV || h % G != 0 || G < 2 || dk_out == nullptr)))
+      (shape == 2 && (kind != bwd::kKindKV || S < 2 || G % S != 0 || h % S != 0 ||
+                      (S == G && dk_out == nullptr))))
     return;
   if (kind == bwd::kKindKV) {
     bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out, dv_out,
@@ -676,19 +681,22 @@ __global__ __launch_bounds__(256) void bwd_gqa_sum_kernel(const uint16_t* __rest
   const int c = (int)(i & 15);
   const long token = r / hkv;
   const int kvh = (int)(r - token * hkv);
-  if (flags != nullptr && flags[token] != 0) return;  // a group item wrote this row itself
-  const int g = hq / hkv;
+  // Partials of this row: G / S of them, S heads apart (S = 1: one per head); S = G: a group
+  // item wrote the row itself.
+  const int S = flags != nullptr ? max((int)flags[token], 1) : 1;
+  if (S >= hq / hkv) return;
+  const int g = hq / hkv, n = g / S;
   const uint16_t* p = src + (token * hq + (long)kvh * g) * kHeadDim + 8 * c;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // All loads of a batch go out before the first add (one memory round trip per 8 heads).
-  for (int x0 = 0; x0 < g; x0 += 8) {
+  // All loads of a batch go out before the first add (one memory round trip per 8 partials).
+  for (int x0 = 0; x0 < n; x0 += 8) {
     u32x4 w[8];
 #pragma unroll
     for (int x = 0; x < 8; ++x)
-      if (x0 + x < g) w[x] = gload16(p + (x0 + x) * kHeadDim);
+      if (x0 + x < n) w[x] = gload16(p + (long)(x0 + x) * S * kHeadDim);
 #pragma unroll
     for (int x = 0; x < 8; ++x)
-      if (x0 + x < g) {
+      if (x0 + x < n) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] += E::to_f32(half_of(w[x], e));
       }

@@ -50,7 +50,7 @@ bool is_plan_kind(int32_t kind) {
 bool is_group_kind(int32_t kind) {
   return kind == VA_PLAN_BWD_GROUPS || kind == VA_PLAN_BWD_GROUPS_ALL;
 }
-int32_t item_head(int32_t d) { return d & (va::kItemPairBit - 1); }
+int32_t item_head(int32_t d) { return d & va::kItemHeadMask; }
 
 std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv,
                              int32_t kind) {
@@ -91,13 +91,19 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
       // 384 queries (18.7 us) ties with a q item over 512 keys (17.3 us), and the XCD layout
       // below deals the heavier ones to the same XCDs in every block.
       // A pair item's halves each take one head over every step: twice a per-head item's steps.
-      // A group item's halves take the G heads' steps in sequence, two per step pair.
+      // A group item's halves take its S heads' steps in sequence, two per step pair; a key tile
+      // takes the largest S whose item fits the cap (bwd_group_heads), G / S items per GQA group.
       for (int32_t k0 = s; k0 < e; k0 += va::kBwdBlockN) {
         const int64_t steps = ((int64_t)e - k0 + va::kBwdBlockQ - 1) / va::kBwdBlockQ;
-        const int64_t group_work = (group * steps + 1) / 2 * 32 + kKvItemCost;
-        if (group_work <= group_cap) {
+        const int sub = group_cap >= 0 ? va::bwd_group_heads(steps, group, group_cap, pairs) : 0;
+        if (sub > 0) {
+          const int64_t work = va::bwd_group_work(steps, sub);
           for (int32_t g = 0; g < hkv; ++g)
-            items.push_back({k0, e, s, va::kItemGroupBit | (g * group), group_work});
+            for (int32_t j = 0; j < group / sub; ++j)
+              items.push_back({k0, e, s,
+                               va::kItemGroupBit | ((sub - 1) << va::kItemHeadsShift) |
+                                   (g * group + j * sub),
+                               work});
           continue;
         }
         for (int32_t g = 0; g < hkv; ++g)

@@ -169,26 +169,26 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
     t = ct - s_tbase[lo];
   };
   // The host planner's work measures (plan.cpp): of a per-head item (w1) and of a pair item (w2)
-  // of the candidate, of a kv candidate's group item (wg).
-  auto works = [&](int doc, int t, int is_q, long& w1, long& w2, long& wg) {
+  // of the candidate; `steps` the query steps of a kv candidate (0 for the others).
+  auto works = [&](int doc, int t, int is_q, long& w1, long& w2, long& steps) {
     const long s = s_bound[doc], e = s_bound[doc + 1];
+    steps = 0;
     if (kind == VA_PLAN_FWD) {
-      w1 = w2 = wg = min(s + (long)(t + 1) * kTile, e) - s;
+      w1 = w2 = min(s + (long)(t + 1) * kTile, e) - s;
     } else if (!is_q) {
-      const long steps = (e - (s + (long)t * kTile) + kBwdBlockQ - 1) / kBwdBlockQ;
+      steps = (e - (s + (long)t * kTile) + kBwdBlockQ - 1) / kBwdBlockQ;
       w1 = (steps + 1) / 2 * 32 + kPlanKvItemCost;
       w2 = steps * 32 + kPlanKvItemCost;
-      wg = (group * steps + 1) / 2 * 32 + kPlanKvItemCost;
     } else {
       const long kv_end = min(s + (long)(t + 1) * kTile, e);
       const long tiles = (kv_end - s + kBwdTileK - 1) / kBwdTileK;
       w1 = (tiles + 1) / 2 * 24 + kPlanQItemCost;
       w2 = (tiles + 1) / 2 * 48 + kPlanQItemCost;
-      wg = LONG_MAX;
     }
   };
-  // Group plans: a kv candidate becomes one group item per GQA group when that item's work is at
-  // most the longest item of the list without groups, or that list's work per CU (plan.cpp).
+  // Group plans: a kv candidate becomes G / S group items per GQA group, S the largest head count
+  // whose item's work is at most the longest item of the list without groups, or that list's
+  // work per CU (bwd_group_heads, as in plan.cpp).
   const bool groups = kind == VA_PLAN_BWD && bwd_groups != 0 && group >= 2;
   long long group_cap = -1;
   if (groups) {
@@ -199,8 +199,8 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       for (int c = tid; c < n_cand; c += PT) {
         int doc, t, is_q;
         decode(c, doc, t, is_q);
-        long w1, w2, wg;
-        works(doc, t, is_q, w1, w2, wg);
+        long w1, w2, steps;
+        works(doc, t, is_q, w1, w2, steps);
         long per = 0;  // the candidate's items over one GQA group
         for (int r = 0; r < (pairs ? (group + 1) / 2 : group); ++r)
           per += (pairs && 2 * r + 1 < group) ? w2 : w1;
@@ -216,17 +216,18 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       group_cap = max(longest, total / kPlanCus);
     }
   }
-  auto is_group = [&](int doc, int t, int is_q) {
-    if (!groups || is_q) return false;
-    long w1, w2, wg;
-    works(doc, t, is_q, w1, w2, wg);
-    return wg <= group_cap;
+  auto group_heads = [&](int doc, int t, int is_q) {  // S of the candidate's group items, or 0
+    if (!groups || is_q) return 0;
+    long w1, w2, steps;
+    works(doc, t, is_q, w1, w2, steps);
+    return bwd_group_heads(steps, group, group_cap, pairs);
   };
   // The work measure in buckets of 8.
   auto bucket = [&](int doc, int t, int is_q) {
-    long w1, w2, wg;
-    works(doc, t, is_q, w1, w2, wg);
-    const long work = is_group(doc, t, is_q) ? wg : (pairs ? w2 : w1);
+    long w1, w2, steps;
+    works(doc, t, is_q, w1, w2, steps);
+    const int sub = group_heads(doc, t, is_q);
+    const long work = sub > 0 ? bwd_group_work(steps, sub) : (pairs ? w2 : w1);
     const long b = work >> 3;
     return (int)(b >= kBuckets ? kBuckets - 1 : b);
   };
@@ -259,14 +260,15 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   // in column j % 8 of block j / 8, which spans 8 G slots (fewer columns in the last block);
   // head r of the group goes to row r. In a pair plan a combo's row r < ceil(G / 2) holds the
   // item of heads 2 r, 2 r + 1 (the last head of an odd group alone) and its other rows stay
-  // empty items; a group candidate's combo holds its group item in row 0, empty items below.
+  // empty items; a group candidate's combo holds its G / S group items (heads S r) in rows
+  // r < G / S, empty items below.
   const long n_combos = (long)n_cand * hkv;
   for (int c = tid; c < n_cand; c += PT) {
     int doc, t, is_q;
     decode(c, doc, t, is_q);
     const long pos = atomicAdd(&s_cnt[bucket(doc, t, is_q)], 1);
     const int s = s_bound[doc], e = s_bound[doc + 1];
-    const bool grouped = is_group(doc, t, is_q);
+    const int sub = group_heads(doc, t, is_q);
     for (int g = 0; g < hkv; ++g) {
       const long combo = pos * hkv + g;
       const long blk = combo / kXcds, col = combo % kXcds;
@@ -274,8 +276,11 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
       for (int r = 0; r < group; ++r) {
         const long slot = blk * kXcds * group + r * ncols + col;
         int4 item = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
-        if (grouped) {
-          item = r == 0 ? int4{s + t * kTile, e, s, kItemGroupBit | (g * group)} : int4{0, 0, 0, 0};
+        if (sub > 0) {
+          item = r < group / sub
+                     ? int4{s + t * kTile, e, s,
+                            kItemGroupBit | ((sub - 1) << kItemHeadsShift) | (g * group + r * sub)}
+                     : int4{0, 0, 0, 0};
         } else if (pairs) {
           const int h2 = 2 * r;
           item = h2 < group ? int4{s + t * kTile, e, s,

@@ -27,11 +27,31 @@ constexpr int kPlanCus = 256;  // compute units the plans balance work over (MI3
 // VA_PLAN_BWD takes two query heads per item (pair items, Hq > Hkv) once the per-head list
 // would be this long (2 (ceil(N / 128) + n_docs) Hq items: every CU then holds several).
 constexpr int kBwdPairMinItems = 1024;
-constexpr int kItemPairBit = 1 << 20;  // item word: kind << 24 | group << 21 | pair << 20 | head
-// A kv item over every query head of a GQA group (group items): its halves walk the G heads'
-// steps in sequence and it writes dK/dV of the key tile at Hkv width, so the tile needs no
-// per-head partials and no GQA sum.
+// Item word: kind << 24 | group << 21 | pair << 20 | (heads - 1) << 12 | head.
+constexpr int kItemPairBit = 1 << 20;
+constexpr int kItemHeadMask = (1 << 12) - 1;  // head < Hq <= 4096
+constexpr int kItemHeadsShift = 12;
+// A kv item over S query heads h .. h + S - 1 of one GQA group (group items, S >= 2 dividing G):
+// its halves walk the S heads' steps in sequence. With S = G it writes dK/dV of the key tile at
+// Hkv width (the tile needs no per-head partials and no GQA sum); with S < G it writes the sum of
+// its S heads into the partial of head h, and the GQA sum adds G / S partials for the tile's rows.
 constexpr int kItemGroupBit = 1 << 21;
+// Planners' work measure of a group item over S heads of a kv tile with `steps` query steps: the
+// halves take ceil(S steps / 2) step pairs.
+__host__ __device__ inline int64_t bwd_group_work(int64_t steps, int s) {
+  return (s * steps + 1) / 2 * 32 + kPlanKvItemCost;
+}
+// The head count of a key tile's group items: the largest S >= 2 dividing G whose group item's
+// work is at most `cap`, or 0 (the tile keeps per-head or pair items). S < G only in long lists
+// (`subsets`: those with pair items, several items per CU), where the total work sets the time:
+// in a short list (config 2) items of S < G over its shorter tiles made the backward slower
+// (measured +3.5%), each as long as the longest items.
+__host__ __device__ inline int bwd_group_heads(int64_t steps, int group, int64_t cap, bool subsets) {
+  for (int s = group; s >= 2; --s)
+    if (group % s == 0 && bwd_group_work(steps, s) <= cap) return s;
+    else if (!subsets) break;
+  return 0;
+}
 // Whether a backward plan of `kind` for these host-known sizes has pair items.
 inline bool bwd_plan_pairs(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t hkv, int kind) {
   if (kind == 2 || hkv <= 0 || hq / hkv < 2) return false;  // VA_PLAN_BWD_HEADS, or no group

@@ -54,7 +54,7 @@ def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
     check_xcd_order(items, hq, hkv, lambda q0, e, s, w: min(q0 + 128, e) - s)
 
 
-HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | group << 21 | pair << 20 | head
+HEAD_MASK = (1 << 12) - 1  # item word: kind << 24 | group << 21 | pair << 20 | (S-1) << 12 | head
 
 
 def check_xcd_order(items, hq, hkv, work_of, per_combo=None):
@@ -94,14 +94,19 @@ def test_backward_plan_deals_every_xcd_the_same_items():
     assert all(m == mixes[0] for m in mixes)
 
 
-def bwd_work(a, e, s, w, g=1):
+def group_heads(w):
+    """S of a group item (its heads h .. h + S - 1)."""
+    return ((w >> 12) & 0xFF) + 1
+
+
+def bwd_work(a, e, s, w):
     """The planners' measure: MFMAs per wave per iteration + item cost (a pair item's halves each
     take every step of one head; a per-head item's halves take alternate steps; a group item's
-    halves alternate over the G heads' steps)."""
+    halves alternate over its S heads' steps)."""
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
         if (w >> 21) & 1:
-            return (g * steps + 1) // 2 * 32 + 39
+            return (group_heads(w) * steps + 1) // 2 * 32 + 39
         return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
     return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * (48 if (w >> 20) & 1 else 24) + 30
 
@@ -158,11 +163,13 @@ def test_backward_plan_covers_every_key_and_query_tile_once(lengths, hq, hkv, ki
 @pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (12, 12), (4, 1)])
 @pytest.mark.parametrize("kind", [_lib.VA_PLAN_BWD_GROUPS, _lib.VA_PLAN_BWD_GROUPS_ALL])
 def test_group_plan_covers_every_tile_once(lengths, hq, hkv, kind):
-    """Group plans: every key tile is covered either by one group item per GQA group (first head
-    of the group, bit 21) or by the VA_PLAN_BWD items of that tile for every head; every query
-    tile by the VA_PLAN_BWD q items. VA_PLAN_BWD_GROUPS groups exactly the key tiles whose group
-    item does no more work than the VA_PLAN_BWD list's longest item or its work per CU (256);
-    VA_PLAN_BWD_GROUPS_ALL all of them; with Hq == Hkv both are VA_PLAN_BWD."""
+    """Group plans: the kv items cover every (key tile, query head) exactly once, a key tile either
+    by group items (bit 21) of S heads each, S >= 2 dividing G, G / S per GQA group, or by the
+    VA_PLAN_BWD items of that tile; the q items are VA_PLAN_BWD's. VA_PLAN_BWD_GROUPS gives a
+    tile the largest S whose group item does no more work than the VA_PLAN_BWD list's longest
+    item or its work per CU (256), and no group item when none does, S < G only in lists long
+    enough to take pair items; VA_PLAN_BWD_GROUPS_ALL gives every tile S = G; with Hq == Hkv both
+    are VA_PLAN_BWD."""
     g = hq // hkv
     cu, items = plan(lengths, hq, hkv, kind)
     _, base = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
@@ -171,26 +178,40 @@ def test_group_plan_covers_every_tile_once(lengths, hq, hkv, kind):
         return
     base_works = [bwd_work(*x) for x in base.tolist()]
     cap = max(max(base_works), sum(base_works) // 256)
-    group_tiles = set()
+    covered, subsets = [], {}
     for a, e, s, w in items.tolist():
+        if w >> 24 != 0:
+            continue
+        h = w & HEAD_MASK
         if (w >> 21) & 1:
-            assert w >> 24 == 0 and (w & HEAD_MASK) % g == 0 and not (w >> 20) & 1
-            group_tiles.add((a, e, s))
-    for a, e, s in {(a, e, s) for a, e, s, w in items.tolist() if w >> 24 == 0}:
-        grouped = kind == _lib.VA_PLAN_BWD_GROUPS_ALL or bwd_work(a, e, s, 1 << 21, g) <= cap
-        assert ((a, e, s) in group_tiles) == grouped, (a, e, s)
-    kept = [tuple(x) for x in base.tolist() if x[3] >> 24 == 1 or tuple(x[:3]) not in group_tiles]
-    grp = [tuple(x) for x in items.tolist() if (x[3] >> 21) & 1]
-    assert sorted(kept + grp) == sorted(map(tuple, items.tolist()))
-    assert sorted(grp) == sorted((a, e, s, (1 << 21) | (k * g)) for a, e, s in group_tiles
-                                 for k in range(hkv))
+            n = group_heads(w)
+            assert n >= 2 and g % n == 0 and h % n == 0 and not (w >> 20) & 1
+            subsets.setdefault((a, e, s), set()).add(n)
+            covered += [(a, x) for x in range(h, h + n)]
+        elif (w >> 20) & 1:
+            covered += [(a, h), (a, h + 1)]
+        else:
+            covered.append((a, h))
+    expected = sorted((t, h) for s0, e0 in zip(cu[:-1], cu[1:]) for t in range(s0, e0, 128)
+                      for h in range(hq))
+    assert sorted(covered) == expected
+    for (a, e, s), ns in subsets.items():
+        assert len(ns) == 1, (a, ns)  # one head count per tile
     bound = 2 * (-(-sum(lengths) // 128) + len(lengths)) * hq
     pairs = bound >= _lib.VA_BWD_PAIR_MIN_ITEMS
+    for a, e, s in {(a, e, s) for a, e, s, w in items.tolist() if w >> 24 == 0}:
+        steps = (e - a + 31) // 32
+        fits = [n for n in range(g, 1, -1) if g % n == 0 and (n * steps + 1) // 2 * 32 + 39 <= cap
+                and (pairs or n == g)]
+        want = g if kind == _lib.VA_PLAN_BWD_GROUPS_ALL else (fits[0] if fits else None)
+        assert subsets.get((a, e, s), {None}) == {want}, (a, e, s, want)
+    plain = [tuple(x) for x in base.tolist() if x[3] >> 24 == 1 or tuple(x[:3]) not in subsets]
+    assert sorted(plain) == sorted(tuple(x) for x in items.tolist() if not (x[3] >> 21) & 1)
 
-    def per_combo(key):  # a group item alone; otherwise as in the VA_PLAN_BWD list
+    def per_combo(key):  # G / S group items; otherwise as in the VA_PLAN_BWD list
         a, e, s, item_kind, _grp, work = key
-        if item_kind == 0 and (a, e, s) in group_tiles:
-            return 1
+        if item_kind == 0 and (a, e, s) in subsets:
+            return g // next(iter(subsets[(a, e, s)]))
         if not pairs:
             return g
         single = bwd_work(a, e, s, item_kind << 24)
@@ -200,7 +221,7 @@ def test_group_plan_covers_every_tile_once(lengths, hq, hkv, kind):
         if pair == single:
             return (g + 1) // 2
         return 1 if work == single else g // 2
-    check_xcd_order(items, hq, hkv, lambda a, e, s, w: bwd_work(a, e, s, w, g), per_combo)
+    check_xcd_order(items, hq, hkv, bwd_work, per_combo)
 
 
 @pytest.mark.parametrize("lengths,pairs", [([512] * 4, False), ([64, 37, 50, 12], False),

@@ -161,8 +161,15 @@ def test_pair_backward_matches_oracle(lengths, hq, hkv, dtype):
     check_all(out.cpu(), tuple(t.cpu() for t in runs[0]), ref, dtype, n, hq)
 
 
+GROUP_CASES = CASES + [([300, 45, 1, 128], 12, 2, "peaky"),
+                       # long enough for pair items: group items of 2, 3 and 6 heads (G = 6), and
+                       # of 7 beside pair tiles (G = 7)
+                       ([300] * 12 + [64] * 10, 12, 2, torch.float16),
+                       ([250] * 10 + [40] * 30, 28, 4, torch.bfloat16)]
+
+
 @pytest.mark.parametrize("kind", ["all", "auto"])
-@pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
+@pytest.mark.parametrize("lengths,hq,hkv,dtype", GROUP_CASES)
 def test_group_backward_matches_oracle(lengths, hq, hkv, dtype, kind):
     """Backward plans with GQA group items (one kv item over all G query heads of a group, writing
     dK/dV at Hkv width): every key tile grouped (VA_PLAN_BWD_GROUPS_ALL), and the planner's mix
@@ -178,9 +185,12 @@ def test_group_backward_matches_oracle(lengths, hq, hkv, dtype, kind):
     cu = np.concatenate([[0], np.cumsum([x for x in lengths if x])]).astype(np.int32)
     code = att._lib.VA_PLAN_BWD_GROUPS_ALL if kind == "all" else att._lib.VA_PLAN_BWD_GROUPS
     items = att.build_plan_host(cu, hq, hkv, code)
+    kv = items[(items[:, 3] >> 24) == 0]
     if hq > hkv and kind == "all":
-        kv = items[(items[:, 3] >> 24) == 0]
         assert len(kv) and ((kv[:, 3] >> 21) & 1).all()
+    if kind == "auto" and len(lengths) == 22:  # the subsets this case exists for
+        heads = {((w >> 12) & 0xFF) + 1 for w in kv[:, 3].tolist() if (w >> 21) & 1}
+        assert heads == {2, 3, 6}, heads
     plan = _Plan(base.fwd_items[: base.n_fwd], torch.from_numpy(items).to(dev), n)
     qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
     out, lse = att.attention_forward(qd, kd, vd, plan, SCALE)
@@ -475,19 +485,19 @@ def test_packed_attention_matches_oracle(dtype):
         assert r <= tol["g"], (name, r)
 
 
-HEAD_MASK = (1 << 20) - 1  # item word: kind << 24 | pair << 20 | head
+HEAD_MASK = (1 << 12) - 1  # item word: kind << 24 | group << 21 | pair << 20 | (S-1) << 12 | head
 
 
-def plan_work(kind, a, e, s, w, g=1):
+def plan_work(kind, a, e, s, w):
     """The planners' work measure of an item: keys visited (forward); MFMAs per wave per
     iteration plus the item's fixed cost (backward; a pair item's halves take every step, a
-    group item's the G heads' steps)."""
+    group item's the steps of its S heads)."""
     if kind == 0:
         return min(a + 128, e) - s
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
         if (w >> 21) & 1:
-            return (g * steps + 1) // 2 * 32 + 39
+            return ((((w >> 12) & 0xFF) + 1) * steps + 1) // 2 * 32 + 39
         return (steps if (w >> 20) & 1 else (steps + 1) // 2) * 32 + 39
     return ((min(a + 128, e) - s + 31) // 32 + 1) // 2 * (48 if (w >> 20) & 1 else 24) + 30
 
@@ -495,7 +505,8 @@ def plan_work(kind, a, e, s, w, g=1):
 def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
     """The items of one (tile, kind, GQA group) sit a constant stride apart, at most 8 (one XCD),
     and the groups come longest first by the work measure in buckets of 8. Empty items (the
-    rows a pair plan or a group item leaves free) are skipped; a group item is its combo alone."""
+    rows a pair plan or group items leave free) are skipped; a tile's G / S group items of S heads
+    form its combo."""
     g = hq // hkv
     combos = {}
     for pos, (a, e, s, w) in enumerate(items.tolist()):
@@ -505,12 +516,16 @@ def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
     firsts = []
     for key, entries in combos.items():
         pos = [p for p, _ in entries]
-        grouped = (entries[0][1] >> 21) & 1
-        assert len(pos) == (1 if grouped else (g if not pairs else (g + 1) // 2)), key
+        w_first = entries[0][1]
+        grouped = (w_first >> 21) & 1
+        n_heads = ((w_first >> 12) & 0xFF) + 1
+        assert len(pos) == (g // n_heads if grouped else (g if not pairs else (g + 1) // 2)), key
         steps = {b - a for a, b in zip(pos, pos[1:])}
         assert len(steps) <= 1 and all(0 < x <= 8 for x in steps), (key, pos)
-        w0 = (key[3] << 24) | ((1 << 20) if pairs and g > 1 and not grouped else 0) | (grouped << 21)
-        firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], w0, g) // 8))
+        w0 = (key[3] << 24) | ((1 << 20) if pairs and g > 1 and not grouped else 0)
+        if grouped:
+            w0 = w_first
+        firsts.append((pos[0], plan_work(kind, key[0], key[1], key[2], w0) // 8))
     work = [w for _, w in sorted(firsts)]
     assert work == sorted(work, reverse=True)
 
@@ -724,7 +739,8 @@ def test_kernels_skip_items_of_a_plan_for_other_sizes():
     """A work list built for more query heads and more tokens than the launch: the kernels skip
     every item whose head or rows fall outside the launch, so nothing is written outside the
     launch's output tensors (each is a view inside a larger NaN-filled buffer whose margins must
-    stay NaN), and the items that do fit still compute their rows correctly."""
+    stay NaN), and the items that do fit still compute their rows correctly (per-head items; the
+    group items of a list built for G = 6 do not fit G = 2 and are skipped: canaries only)."""
     banner("mismatched plan")
     dev = torch.device("cuda")
     small, big = [200, 100], [200, 100, 300]
@@ -750,10 +766,12 @@ def test_kernels_skip_items_of_a_plan_for_other_sizes():
     wb, ws = canaried((ws_bytes,), torch.uint8)
     kb, dk = canaried((n, hkv, 128), torch.float16)
     vb, dv = canaried((n, hkv, 128), torch.float16)
-    att.check(lib.va_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                         lse.data_ptr(), plan_big.bwd_items.data_ptr(), plan_big.n_bwd, n,
-                         hq_small, hkv, 128, SCALE, 0, dq.data_ptr(), dk.data_ptr(),
-                         dv.data_ptr(), ws.data_ptr(), ws_bytes, att._stream()), "va_bwd")
+    part_items, n_part = plan_big.partial_bwd()
+    for items_b, n_b in ((plan_big.bwd_items, plan_big.n_bwd), (part_items, n_part)):
+        att.check(lib.va_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                             out.data_ptr(), lse.data_ptr(), items_b.data_ptr(), n_b, n,
+                             hq_small, hkv, 128, SCALE, 0, dq.data_ptr(), dk.data_ptr(),
+                             dv.data_ptr(), ws.data_ptr(), ws_bytes, att._stream()), "va_bwd")
     torch.cuda.synchronize()
     for buf in (ob, lb, qb, kb, vb):
         assert torch.isnan(buf[:pad].float()).all() and torch.isnan(buf[-pad:].float()).all()
