@@ -71,15 +71,16 @@ int32_t va_head_dim(void);
  * and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the heads
  * sharing K/V run on one XCD and share its L2. Fully masked causal tiles and cross-document tiles
  * never appear. VA_PLAN_BWD_GROUPS is VA_PLAN_BWD with GQA group items where they do not lengthen
- * the plan: a key tile whose dK/dV item over all G query heads of a group does no more work than
- * the longest item of the VA_PLAN_BWD list, or than the list's work per CU (256 CUs), gets one
- * such item per GQA group instead of its per-head or pair items; it writes that tile's dK/dV
- * itself (Hkv width), with no per-head partials and nothing for the GQA sum to do there.
- * VA_PLAN_BWD_GROUPS_ALL makes every key tile a group tile. Group plans need dk/dv in va_bwd
- * (group items have no per-head partials to leave behind) and Hq > Hkv, and are built on the
- * host only. Every plan kind gives the same outputs up to rounding (a pair item sums a head's
- * steps or tiles in one sequence instead of two halves, a group item the G heads' in one); each
- * is deterministic.
+ * the plan: a key tile gets, per GQA group, G / S kv items over S query heads each (S >= 2
+ * dividing G: the largest whose item does no more work than the longest item of the VA_PLAN_BWD
+ * list, or than that list's work per CU (256 CUs); S < G only in lists with pair items). An item
+ * of S = G heads writes the tile's dK/dV itself (Hkv width): no per-head partials, nothing for
+ * the GQA sum; one of S < G heads writes the sum of its heads into the first head's partial.
+ * Item word: kind << 24 | group << 21 | pair << 20 | (S - 1) << 12 | head.
+ * VA_PLAN_BWD_GROUPS_ALL gives every key tile S = G. Group plans need dk/dv in va_bwd (their
+ * partials are not per head) and Hq > Hkv. Every plan kind gives the same outputs up to rounding
+ * (a pair item sums a head's steps or tiles in one sequence instead of two halves, a group item
+ * its heads' in one); each is deterministic.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
 int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                  int64_t* n_items);
