@@ -531,7 +531,8 @@ def check_device_xcd_layout(items, kind, hq, hkv, pairs=False):
 
 
 @pytest.mark.parametrize("lengths", [[64, 37, 50, 12], [334, 0, 200, 100, 7], [1000, 24],
-                                     [1, 1, 1, 2, 3], [512] * 4])
+                                     [1, 1, 1, 2, 3], [512] * 4,
+                                     [300] * 12 + [64] * 10])  # pair list: group items of 2, 3, 6
 def test_device_plan_matches_host_plan(lengths):
     """The plans built on the device from device lengths hold the host plans' items (as a set: the
     order inside a work bucket is free) in the same XCD layout, then empty items up to their
@@ -546,15 +547,16 @@ def test_device_plan_matches_host_plan(lengths):
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     assert dplan.cu.cpu().numpy().tolist() == cu.tolist()
     groups = att._lib.VA_PLAN_BWD_GROUPS
+    pairs = 2 * (-(-n // 128) + len(lengths)) * hq >= att._lib.VA_BWD_PAIR_MIN_ITEMS
     part_items, part_n = dplan.partial_bwd()
     for kind, items, count in ((0, dplan.fwd_items, dplan.n_fwd), (1, part_items, part_n),
                                (groups, dplan.bwd_items, dplan.n_bwd)):
         host = att.build_plan_host(cu, hq, hkv, kind)
         got = items.cpu().numpy()[:count]
-        if kind == groups:  # group combos leave their other rows empty
+        if kind == groups or (kind == 1 and pairs):  # rows left empty inside the blocks
             real = [tuple(x) for x in got.tolist() if any(x)]
             assert sorted(real) == sorted(map(tuple, host.tolist()))
-            check_device_xcd_layout(got, kind, hq, hkv)
+            check_device_xcd_layout(got, kind, hq, hkv, pairs=pairs)
         else:
             real, empty = got[: len(host)], got[len(host):]
             assert sorted(map(tuple, real.tolist())) == sorted(map(tuple, host.tolist()))
@@ -590,7 +592,7 @@ def test_device_plan_matches_host_plan(lengths):
     got = all_items.cpu().numpy()[:count]
     host = att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_BWD_GROUPS_ALL)
     assert sorted(tuple(x) for x in got.tolist() if any(x)) == sorted(map(tuple, host.tolist()))
-    check_device_xcd_layout(got, 1, hq, hkv)
+    check_device_xcd_layout(got, 1, hq, hkv, pairs=pairs)
 
 
 def test_device_lengths_plan_is_rebuilt_inside_a_captured_graph():
