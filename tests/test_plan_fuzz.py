@@ -1,0 +1,64 @@
+"""Randomised checks of the host planner (no GPU): for random document lengths (zero-length
+documents included), head shapes and every plan kind, the work items cover every (tile, query
+head) of the forward, and every (key tile, head) and (query tile, head) of the backward, exactly
+once; every item lies inside its document; and va_plan_size agrees with va_plan_build. The
+fixed-case tests in test_abi.py pin the ordering and the planners' rules; these look for
+coverage holes and double counting over many more shapes."""
+
+import numpy as np
+from hypothesis import given, settings, strategies as st
+
+from hackaton_amd import _lib
+from hackaton_amd.attention import build_plan_host
+
+HEADS = [(12, 2), (28, 4), (4, 1), (12, 12), (6, 3), (14, 2)]
+KINDS = [_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD, _lib.VA_PLAN_BWD_HEADS, _lib.VA_PLAN_BWD_PAIRS,
+         _lib.VA_PLAN_BWD_GROUPS, _lib.VA_PLAN_BWD_GROUPS_ALL]
+
+
+def heads_of(w, hq, hkv):
+    """Query heads an item covers (item word: kind << 24 | group << 21 | pair << 20 |
+    (S - 1) << 12 | head)."""
+    h = w & 0xFFF
+    if (w >> 21) & 1:
+        n = ((w >> 12) & 0xFF) + 1
+        g = hq // hkv
+        assert n >= 2 and g % n == 0 and h % n == 0
+        return list(range(h, h + n))
+    assert (w >> 12) & 0xFF == 0
+    if (w >> 20) & 1:
+        assert (h + 1) // (hq // hkv) == h // (hq // hkv)
+        return [h, h + 1]
+    return [h]
+
+
+@settings(max_examples=150, deadline=None)
+@given(lengths=st.lists(st.one_of(st.integers(0, 3), st.integers(1, 700)), min_size=1,
+                        max_size=24),
+       shape=st.sampled_from(HEADS), kind=st.sampled_from(KINDS))
+def test_plans_cover_every_tile_and_head_once(lengths, shape, kind):
+    hq, hkv = shape
+    if sum(lengths) == 0:
+        lengths = lengths + [1]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    items = build_plan_host(cu, hq, hkv, kind)
+    n = np.zeros(1, dtype=np.int64)
+    assert _lib.lib().va_plan_size(np.ascontiguousarray(cu).ctypes.data_as(_lib._pi32),
+                                   len(lengths), hq, hkv, kind,
+                                   n.ctypes.data_as(_lib._pi64)) == 0
+    assert int(n[0]) == len(items)
+    docs = [(int(s), int(e)) for s, e in zip(cu[:-1], cu[1:]) if e > s]
+    tiles = sorted((t, h) for s, e in docs for t in range(s, e, 128) for h in range(hq))
+    seen = {0: [], 1: []}
+    for a, e, s, w in items.tolist():
+        assert (s, e) in docs and s <= a < e and (a - s) % 128 == 0
+        item_kind = w >> 24
+        assert item_kind in (0, 1)
+        if kind == _lib.VA_PLAN_FWD:
+            assert w == (w & 0xFFF)  # a plain head
+        seen[item_kind] += [(a, h) for h in heads_of(w, hq, hkv)]
+        assert all(h < hq for _, h in seen[item_kind][-1:])
+    if kind == _lib.VA_PLAN_FWD:
+        assert sorted(seen[0]) == tiles and not seen[1]
+    else:
+        assert sorted(seen[0]) == tiles and sorted(seen[1]) == tiles
