@@ -103,8 +103,8 @@ __device__ __forceinline__ void bwd_kv_item(
   }
 
   const int n_steps = (doc_end - k0 + BQ - 1) / BQ;
-  // Units of work: (head, step) in head-major order, over one head or (group items) the G heads
-  // of the group. Iterations of the step loop: a pair of units (the halves take alternate units),
+  // Units of work: (head, step) in head-major order, over one head or (group items) the S heads
+  // h .. h + S - 1. Iterations of the step loop: a pair of units (the halves take alternate units),
   // or one step of each head of a pair item.
   const int n_units = S * n_steps;
   const int n_iter = pair ? n_steps : (n_units + 1) / 2;
