@@ -59,7 +59,8 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
   const int32_t group = hq / hkv, rows = pairs ? (group + 1) / 2 : group;
   // Group plans: the largest group-item work that keeps the plan about as long as its VA_PLAN_BWD
   // form: that list's longest item, or its work per CU when that is more (measured at configs
-  // 3-5: half the work per CU left config 4 7% slower, all key tiles grouped config 3 50%).
+  // 3-5: half the work per CU as the bound left config 4 7% slower, the longest item alone 8%;
+  // 1.5x and 2x the work per CU made config 3 26% and 59% slower, every key tile at S = G 50%).
   int64_t group_cap = -1;
   if (is_group_kind(kind) && group >= 2) {
     if (kind == VA_PLAN_BWD_GROUPS_ALL) {
