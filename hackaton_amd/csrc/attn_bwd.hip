@@ -67,7 +67,10 @@ __device__ __host__ constexpr int block_c(int b, int /*i*/) { return b; }
 // of one GQA group: then half j takes head h + j over every query step, so the halves share the
 // K/V tile, never exchange accumulators, and each writes both partials of its head.
 // --------------------------------------------------------------------------------------------
-template <class E>
+// SHAPE (item word bits 20-21): 0 per head, 1 pair, 2 group; a template constant, so that each
+// shape's step loop carries no unit / head arithmetic of the others (per-head items: no division
+// by the step count, no pair selects).
+template <class E, int SHAPE>
 __device__ __forceinline__ void bwd_kv_item(
     lds_u16* smem, float (&stat)[2][2][2][bwd::BQ], const int4 it,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -78,9 +81,9 @@ __device__ __forceinline__ void bwd_kv_item(
     float scale, float scale_log2) {
   using namespace bwd;
   const int k0 = it.x, doc_end = it.y, h = it.w & kHeadMask;
-  const bool pair = (it.w >> 20) & 1;
+  constexpr bool pair = SHAPE == 1;
   // Group items walk heads h .. h + S - 1 in sequence (S = G: the whole GQA group).
-  const bool grouped = (it.w >> 21) & 1;
+  constexpr bool grouped = SHAPE == 2;
   const int S = grouped ? ((it.w >> kItemHeadsShift) & 0xff) + 1 : 1;
   const int G = hq / hkv;
   const int kvh = h / G;
@@ -109,8 +112,12 @@ __device__ __forceinline__ void bwd_kv_item(
   const int n_units = S * n_steps;
   const int n_iter = pair ? n_steps : (n_units + 1) / 2;
   auto unit_of = [&](int p, int j) { return min(2 * p + j, n_units - 1); };  // clamped: loads
-  auto step_of = [&](int p, int j) { return pair ? p : unit_of(p, j) % n_steps; };
-  auto head_of = [&](int p, int j) { return pair ? h + j : h + unit_of(p, j) / n_steps; };
+  auto step_of = [&](int p, int j) {
+    return pair ? p : grouped ? unit_of(p, j) % n_steps : unit_of(p, j);
+  };
+  auto head_of = [&](int p, int j) {
+    return pair ? h + j : grouped ? h + unit_of(p, j) / n_steps : h;
+  };
   auto live = [&](int p, int j) {  // the unit exists and has queries at or after this strip's keys
     if (!pair && 2 * p + j >= n_units) return false;
     return kw0 <= k0 + step_of(p, j) * BQ + BQ - 1;
@@ -325,7 +332,7 @@ __device__ __forceinline__ void bwd_kv_item(
   // row's dK/dV itself): every key row belongs to one tile, whose items of the GQA group's first
   // head write its flag.
   if (flags != nullptr && h % G == 0 && tid < BK && k0 + tid < doc_end) flags[k0 + tid] = S;
-  if (pair) {
+  if constexpr (pair) {
     // Each half holds the whole dK/dV of its head: both go out through this wave's own row tile
     // (the LDS stages are free after the loop's last barrier), dK scaled.
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar: no VGPR kept
@@ -371,7 +378,7 @@ __device__ __forceinline__ void bwd_kv_item(
 // one GQA group: then half j takes head h + j over both tiles of every pair, so the halves share
 // the K/V tiles, never exchange dQ, and each writes all 128 columns of its head.
 // --------------------------------------------------------------------------------------------
-template <class E>
+template <class E, bool PAIR>
 __device__ __forceinline__ void bwd_q_item(
     lds_u16* smem, const int4 it, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -380,7 +387,7 @@ __device__ __forceinline__ void bwd_q_item(
     float scale, float scale_log2, float* stat_f) {
   using namespace bwd;
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kHeadMask;
-  const bool pair = (it.w >> 20) & 1;
+  constexpr bool pair = PAIR;
   const int kvh = h / (hq / hkv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
   const int half = wave / NS, strip = wave % NS;
@@ -648,11 +655,21 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
                       (S == G && dk_out == nullptr))))
     return;
   if (kind == bwd::kKindKV) {
-    bwd_kv_item<E>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out, dv_out,
-                   flags, n_tokens, hq, hkv, scale, scale_log2);
+    if (shape == 0)
+      bwd_kv_item<E, 0>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                        dv_out, flags, n_tokens, hq, hkv, scale, scale_log2);
+    else if (shape == 1)
+      bwd_kv_item<E, 1>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                        dv_out, flags, n_tokens, hq, hkv, scale, scale_log2);
+    else
+      bwd_kv_item<E, 2>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                        dv_out, flags, n_tokens, hq, hkv, scale, scale_log2);
+  } else if (shape == 0) {
+    bwd_q_item<E, false>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
+                         scale_log2, qstat);
   } else {
-    bwd_q_item<E>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale, scale_log2,
-                  qstat);
+    bwd_q_item<E, true>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
+                        scale_log2, qstat);
   }
 }
 
