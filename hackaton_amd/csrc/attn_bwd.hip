@@ -112,15 +112,45 @@ __device__ __forceinline__ void bwd_kv_item(
   const int n_units = S * n_steps;
   const int n_iter = pair ? n_steps : (n_units + 1) / 2;
   auto unit_of = [&](int p, int j) { return min(2 * p + j, n_units - 1); };  // clamped: loads
+  // Group items decode unit 2 p + j into (head offset, step) without a division per iteration:
+  // nx_* hold the two units of the iteration whose rows are loaded next and advance by two units
+  // per iteration (at most two head changes, n_steps >= 1); cur_* hold the computed iteration's.
+  // A head offset of S or more is past the last unit (loads take the last unit's rows).
+  int nx_ho[2] = {0, n_steps > 1 ? 0 : 1}, nx_s[2] = {0, n_steps > 1 ? 1 : 0};
+  int cur_ho[2] = {0, 0}, cur_s[2] = {0, 0};
+  auto advance2 = [&](int& ho, int& st) {
+    st += 2;
+    if (st >= n_steps) {
+      st -= n_steps;
+      ++ho;
+    }
+    if (st >= n_steps) {
+      st -= n_steps;
+      ++ho;
+    }
+  };
+  // Step and head of unit j of iteration p (grouped: of the iteration loaded next).
   auto step_of = [&](int p, int j) {
-    return pair ? p : grouped ? unit_of(p, j) % n_steps : unit_of(p, j);
+    if constexpr (grouped) return nx_ho[j] < S ? nx_s[j] : n_steps - 1;
+    else return pair ? p : unit_of(p, j);
   };
   auto head_of = [&](int p, int j) {
-    return pair ? h + j : grouped ? h + unit_of(p, j) / n_steps : h;
+    if constexpr (grouped) return h + min(nx_ho[j], S - 1);
+    else return pair ? h + j : h;
   };
-  auto live = [&](int p, int j) {  // the unit exists and has queries at or after this strip's keys
-    if (!pair && 2 * p + j >= n_units) return false;
-    return kw0 <= k0 + step_of(p, j) * BQ + BQ - 1;
+  // The computed iteration p's unit j: its step, and whether it exists and has queries at or
+  // after this strip's keys.
+  auto cur_step = [&](int p, int j) {
+    if constexpr (grouped) return cur_s[j];
+    else return step_of(p, j);
+  };
+  auto live = [&](int p, int j) {
+    if constexpr (grouped) {
+      if (cur_ho[j] >= S) return false;
+    } else if (!pair && 2 * p + j >= n_units) {
+      return false;
+    }
+    return kw0 <= k0 + cur_step(p, j) * BQ + BQ - 1;
   };
 
   // Staging of a step pair: thread chunk i is (step half i >> 1, tensor i & 1 = Q / dO), row
@@ -194,8 +224,16 @@ __device__ __forceinline__ void bwd_kv_item(
   __syncthreads();
   for (int p = 0; p < n_iter; ++p) {
     const int stage = p & 1;
+    if constexpr (grouped) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        cur_ho[j] = nx_ho[j];
+        cur_s[j] = nx_s[j];
+        advance2(nx_ho[j], nx_s[j]);
+      }
+    }
     if (p + 1 < n_iter) gload_pair(p + 1);
-    const int qs0 = k0 + step_of(p, half) * BQ;
+    const int qs0 = k0 + cur_step(p, half) * BQ;
     if (live(p, half)) {
       const lds_u16* qs = smem + KV_OFF_Q + (stage * 2 + half) * ROWT;
       const lds_u16* dos = smem + KV_OFF_DO + (stage * 2 + half) * ROWT;
