@@ -320,7 +320,9 @@ class Workload:
         if stage < 0 and not self.gqa_sum_launched():  # the plan's group items write dK/dV
             self._lib.check(self.lib.va_bwd_stage(self._lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
         elif stage < 0:
-            self._lib.check(self.lib.va_bwd(*argv), "va_bwd")
+            self._lib.check(self.lib.va_bwd_stage(self._lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
+            self._lib.check(self.lib.va_bwd_stage(self.plan.bwd_finish_stage, *argv),
+                            "va_bwd_stage")
         else:
             self._lib.check(self.lib.va_bwd_stage(stage, *argv), "va_bwd_stage")
 
@@ -365,7 +367,7 @@ class Workload:
         for name, launch in ((fwd_name, self.fwd),
                              ("bwd_kernel", lambda s, st: self.bwd(s, st, lib.VA_BWD_MAIN)),
                              ("bwd_gqa_sum_kernel",
-                              lambda s, st: self.bwd(s, st, lib.VA_BWD_FINISH))):
+                              lambda s, st: self.bwd(s, st, self.plan.bwd_finish_stage))):
             if name == "bwd_gqa_sum_kernel" and not self.gqa_sum_launched():
                 continue
             g = self.graph(launch)
@@ -502,7 +504,7 @@ def main(argv=None):
             w.bwd(s, stream, w._lib.VA_BWD_MAIN)
         if w.gqa_sum_launched():
             for s in w.sets:
-                w.bwd(s, stream, w._lib.VA_BWD_FINISH)
+                w.bwd(s, stream, w.plan.bwd_finish_stage)
         torch.cuda.synchronize()
         print(json.dumps({"pmc_probe": cfg["name"], "copy_read_bytes": x.numel() * 4,
                           "copy_write_bytes": y.numel() * 4, "launches_per_kernel": len(w.sets)}),

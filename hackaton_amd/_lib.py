@@ -15,7 +15,7 @@ VA_PLAN_FWD, VA_PLAN_BWD, VA_PLAN_BWD_HEADS, VA_PLAN_BWD_PAIRS = 0, 1, 2, 3
 VA_PLAN_BWD_GROUPS, VA_PLAN_BWD_GROUPS_ALL = 4, 5
 VA_BWD_PAIR_MIN_ITEMS = 1024
 VA_LAYOUT_PACKED, VA_LAYOUT_PADDED = 0, 1
-VA_BWD_MAIN, VA_BWD_FINISH = 1, 2
+VA_BWD_MAIN, VA_BWD_FINISH, VA_BWD_FINISH_HEADS = 1, 2, 3
 VA_FWD_MANY_ITEMS = 512
 
 _p = ctypes.c_void_p

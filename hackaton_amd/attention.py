@@ -94,7 +94,7 @@ class Plan:
     without them."""
 
     __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "offsets", "_hq", "_hkv",
-                 "_part", "bwd_finish")
+                 "_part", "bwd_finish", "bwd_finish_stage")
 
     def __init__(self, offsets, hq, hkv, device):
         cu = np.ascontiguousarray(np.asarray(offsets, dtype=np.int32))
@@ -111,8 +111,12 @@ class Plan:
         # whether the backward needs its GQA sum: not when every key tile's group items take the
         # whole GQA group (item word: group bit 21, heads - 1 in bits 12-19)
         kv = host_bwd[(host_bwd[:, 3] >> 24) == 0]
-        whole = (((kv[:, 3] >> 21) & 1) == 1) & ((((kv[:, 3] >> 12) & 0xFF) + 1) == hq // hkv)
+        grouped = ((kv[:, 3] >> 21) & 1) == 1
+        whole = grouped & ((((kv[:, 3] >> 12) & 0xFF) + 1) == hq // hkv)
         self.bwd_finish = hq > hkv and not bool(whole.all())
+        # the GQA sum of a list without group items reads no row flags (VA_BWD_FINISH_HEADS)
+        self.bwd_finish_stage = _lib.VA_BWD_FINISH if bool(grouped.any()) else \
+            _lib.VA_BWD_FINISH_HEADS
 
     def partial_bwd(self):
         """(items, n) of the backward list without group items (built on first use)."""
@@ -147,7 +151,7 @@ class DevicePlan:
     sizes bound; its slots past the real items are empty items that the kernels skip."""
 
     __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "cu", "_part",
-                 "bwd_finish", "__weakref__")
+                 "bwd_finish", "bwd_finish_stage", "__weakref__")
 
     def __init__(self, lengths, n_tokens, hq, hkv):
         lengths = lengths.reshape(-1)
@@ -174,6 +178,7 @@ class DevicePlan:
         self._part = (part, self.n_bwd)
         self.bwd_items = part
         self.bwd_finish = hq > hkv  # the device list's group tiles are not known here
+        self.bwd_finish_stage = _lib.VA_BWD_FINISH
         if hq > hkv and n_docs > 0:
             self.bwd_items = torch.empty_like(part)
             check(lib().va_plan_build_device(self.cu.data_ptr(), n_docs, n_tokens, hq, hkv,
@@ -285,6 +290,9 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws) if ws.numel() else None, ws.numel(), _stream())
     if outputs and not getattr(plan, "bwd_finish", True):  # group items wrote every dK/dV row
         check(lib().va_bwd_stage(_lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
+    elif outputs and getattr(plan, "bwd_finish_stage", None) == _lib.VA_BWD_FINISH_HEADS:
+        check(lib().va_bwd_stage(_lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
+        check(lib().va_bwd_stage(_lib.VA_BWD_FINISH_HEADS, *argv), "va_bwd_stage")
     else:
         check(lib().va_bwd(*argv), "va_bwd")
     if outputs:

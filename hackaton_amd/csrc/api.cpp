@@ -153,7 +153,7 @@ extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, cons
                             int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype,
                             void* dq, void* dk, void* dv, void* workspace,
                             int64_t workspace_bytes, void* stream) {
-  if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH)
+  if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH && stage != VA_BWD_FINISH_HEADS)
     return va::fail(VA_EINVAL, "va_bwd_stage: stage %d", stage);
   return va::bwd_checked(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
                          head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);

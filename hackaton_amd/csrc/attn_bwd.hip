@@ -771,21 +771,24 @@ static hipError_t launch_bwd_main_t(const BwdArgs& a) {
   return hipGetLastError();
 }
 
+// heads_only: the list has no group items, every row sums its G per-head partials (flags unread).
 template <class E>
-static hipError_t launch_bwd_finish_t(const BwdArgs& a) {
+static hipError_t launch_bwd_finish_t(const BwdArgs& a, bool heads_only) {
   if (a.dk == nullptr || a.dk_part == a.dk) return hipSuccess;  // partials are the result
   const long n8 = a.n_tokens * a.hkv * kHeadDim / 8;
   if (n8 == 0) return hipSuccess;
   hipLaunchKernelGGL(bwd_gqa_sum_kernel<E>, dim3((unsigned)((2 * n8 + 255) / 256)), dim3(256), 0,
                      a.stream, (const uint16_t*)a.dk_part, (const uint16_t*)a.dv_part,
-                     (uint16_t*)a.dk, (uint16_t*)a.dv, n8, a.hq, a.hkv, a.flags);
+                     (uint16_t*)a.dk, (uint16_t*)a.dv, n8, a.hq, a.hkv,
+                     heads_only ? nullptr : a.flags);
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_stage(const BwdArgs& a, int stage) {
   const bool bf = a.dtype != 0;
   if (stage == 1) return bf ? launch_bwd_main_t<BF16>(a) : launch_bwd_main_t<F16>(a);
-  return bf ? launch_bwd_finish_t<BF16>(a) : launch_bwd_finish_t<F16>(a);
+  const bool heads_only = stage == 3;
+  return bf ? launch_bwd_finish_t<BF16>(a, heads_only) : launch_bwd_finish_t<F16>(a, heads_only);
 }
 
 hipError_t launch_bwd(const BwdArgs& a) {

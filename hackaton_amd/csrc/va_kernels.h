@@ -123,7 +123,7 @@ struct RopeArgs {
 
 hipError_t launch_fwd(const FwdArgs& a);
 hipError_t launch_bwd(const BwdArgs& a);
-hipError_t launch_bwd_stage(const BwdArgs& a, int stage);  // 1 main, 2 finish
+hipError_t launch_bwd_stage(const BwdArgs& a, int stage);  // 1 main, 2 finish, 3 finish (no flags)
 hipError_t launch_rope_fwd(const RopeArgs& a);
 hipError_t launch_rope_bwd(const RopeArgs& a);
 hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t* t_idx,

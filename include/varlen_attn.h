@@ -55,7 +55,7 @@ enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1, VA_PLAN_BWD_HEADS = 2, VA_PLAN_BWD_PAIR
        VA_PLAN_BWD_GROUPS = 4, VA_PLAN_BWD_GROUPS_ALL = 5 };
 enum { VA_BWD_PAIR_MIN_ITEMS = 1024 };
 enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
-enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2 };
+enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2, VA_BWD_FINISH_HEADS = 3 };
 
 const char* va_last_error(void);
 int32_t va_abi_version(void);
@@ -166,8 +166,12 @@ int va_bwd_noalloc(const void* dout, const void* q, const void* k, const void* v
 
 /* The same backward in its two stages, for callers that time or overlap them separately:
  * VA_BWD_MAIN (dQ and the per-head dK/dV partials) and VA_BWD_FINISH (the GQA sums into dk/dv;
- * nothing when they are NULL or Hq == Hkv). Any other stage value is VA_EINVAL. Same arguments
- * as va_bwd.
+ * nothing when they are NULL or Hq == Hkv). VA_BWD_FINISH_HEADS is VA_BWD_FINISH for a list
+ * without group items (VA_PLAN_BWD, VA_PLAN_BWD_HEADS, VA_PLAN_BWD_PAIRS, or a VA_PLAN_BWD_GROUPS
+ * list in which the planner grouped no key tile): every key row then sums its G per-head
+ * partials, so the row flags that group items leave are not read (one dependent memory round
+ * trip less); after a list with group items it would sum stale partials. Any other stage value
+ * is VA_EINVAL. Same arguments as va_bwd.
  * Replaces: the same reference call as va_bwd (solution/attention.py:230-232). */
 int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k, const void* v,
                  const void* out, const float* lse, const int32_t* items, int64_t n_items,

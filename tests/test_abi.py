@@ -291,7 +291,7 @@ def test_attention_entry_points_validate_before_launching():
     rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, fake,
                     fake, None, fake, nbytes.value, None)
     assert rc == _lib.VA_EINVAL and b"both" in lib.va_last_error()
-    for stage in (0, 3):  # only VA_BWD_MAIN and VA_BWD_FINISH exist
+    for stage in (0, 4):  # only VA_BWD_MAIN, VA_BWD_FINISH and VA_BWD_FINISH_HEADS exist
         rc = lib.va_bwd_stage(stage, fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128,
                               0.1, 0, fake, fake, fake, fake, nbytes.value, None)
         assert rc == _lib.VA_EINVAL and b"stage" in lib.va_last_error()

@@ -793,3 +793,45 @@ def test_kernels_skip_items_of_a_plan_for_other_sizes():
         assert torch.isnan(buf[:pad].float()).all() and torch.isnan(buf[-pad:].float()).all()
     err_o = float(np.max(np.abs(out2.cpu().float().numpy() - ref[0])))
     assert err_o <= TOL[torch.float16]["o"], err_o
+
+
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_gqa_sum_without_flags_matches_flagged_sum(cfg):
+    """VA_BWD_FINISH_HEADS (the GQA sum that reads no row flags) on a list without group items
+    gives bitwise the flagged sum's dK/dV; the plans choose it exactly when their backward list has
+    no group items (configuration 2's list; configuration 3's has group tiles)."""
+    lengths, c = wl.config_lengths(cfg), wl.CONFIGS[cfg]
+    hq, hkv = c["hq"], c["hkv"]
+    banner("flag-free GQA sum", cfg, len(lengths))
+    dev = torch.device("cuda")
+    plan = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
+    lib = att.lib()
+    if cfg == 3:
+        assert plan.bwd_finish_stage == att._lib.VA_BWD_FINISH
+        items, n_items = plan.partial_bwd()  # the same documents without group items
+    else:
+        assert plan.bwd_finish_stage == att._lib.VA_BWD_FINISH_HEADS
+        items, n_items = plan.bwd_items, plan.n_bwd
+    n = sum(lengths)
+    q, k, v, do = (t.to(dev) for t in wl.make_inputs(lengths, hq, hkv, torch.float16, seed=4))
+    out = torch.empty_like(q)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+    att.check(lib.va_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                         plan.fwd_items.data_ptr(), plan.n_fwd, n, hq, hkv, 128, SCALE, 0,
+                         att._stream()), "va_fwd")
+    ws = att.bwd_workspace(n, hq, hkv, dev)[0]
+    dq = torch.empty_like(q)
+    res = []
+    for stage in (att._lib.VA_BWD_FINISH, att._lib.VA_BWD_FINISH_HEADS):
+        dk, dv = torch.full_like(k, float("nan")), torch.full_like(v, float("nan"))
+        argv = (do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                lse.data_ptr(), items.data_ptr(), n_items, n, hq, hkv, 128, SCALE, 0,
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
+                att._stream())
+        att.check(lib.va_bwd_stage(att._lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
+        att.check(lib.va_bwd_stage(stage, *argv), "va_bwd_stage")
+        res.append((dk, dv))
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert not torch.isnan(a.float()).any()
+        assert torch.equal(a, b)
