@@ -159,26 +159,30 @@ __device__ __forceinline__ void bwd_kv_item(
   // until the store, where its dot product with the dO chunk gives delta = rowsum(dO * O): the
   // loads are then complete and the dot product does not stall the step.
   const int s_row = tid >> 4, s_col = 8 * (tid & 15);
-  const int s_voff = (s_row * (int)qrow + s_col) * 2;  // + the head's column, per step half
+  const int s_voff = (s_row * (int)qrow + s_col) * 2;  // from the unit's (first row, head)
   u32x4 sreg[4], oreg[2];
   float st_lse = 0.f;
   int st_row = 0;
   auto gload_pair = [&](int p) {
+    int row0[2];
+    const float* lrow[2];
 #pragma unroll
     for (int sh = 0; sh < 2; ++sh) {
+      // The unit's head column is in the descriptor's base (wave-uniform), so the per-lane offset
+      // is the same for every unit.
       const int hs = head_of(p, sh);
-      const int qs0 = k0 + min(step_of(p, sh), n_steps - 1) * BQ;
-      const long base = (long)qs0 * qrow;
-      const long bytes = ((long)(doc_end - qs0 - 1) * qrow + (long)(hs + 1) * D) * 2;
-      const int voff = s_voff + hs * D * 2;
-      sreg[2 * sh] = bload16(make_rsrc(q + base, bytes), voff);
-      sreg[2 * sh + 1] = bload16(make_rsrc(dout + base, bytes), voff);
-      oreg[sh] = bload16(make_rsrc(out + base, bytes), voff);
+      row0[sh] = k0 + min(step_of(p, sh), n_steps - 1) * BQ;
+      lrow[sh] = lse + (long)hs * n_tokens;
+      const long base = (long)row0[sh] * qrow + (long)hs * D;
+      const long bytes = ((long)(doc_end - row0[sh] - 1) * qrow + D) * 2;
+      sreg[2 * sh] = bload16(make_rsrc(q + base, bytes), s_voff);
+      sreg[2 * sh + 1] = bload16(make_rsrc(dout + base, bytes), s_voff);
+      oreg[sh] = bload16(make_rsrc(out + base, bytes), s_voff);
     }
     if (tid < 64) {  // raw value: scaled at the store, so that no wait follows the loads here
       const int sh = tid >> 5;
-      st_row = k0 + min(step_of(p, sh), n_steps - 1) * BQ + (tid & 31);
-      st_lse = lse[(long)head_of(p, sh) * n_tokens + min(st_row, doc_end - 1)];
+      st_row = (sh ? row0[1] : row0[0]) + (tid & 31);
+      st_lse = (sh ? lrow[1] : lrow[0])[min(st_row, doc_end - 1)];
     }
   };
   auto store_pair = [&](int stage) {
