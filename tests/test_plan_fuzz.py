@@ -62,3 +62,35 @@ def test_plans_cover_every_tile_and_head_once(lengths, shape, kind):
         assert sorted(seen[0]) == tiles and not seen[1]
     else:
         assert sorted(seen[0]) == tiles and sorted(seen[1]) == tiles
+
+
+def test_flag_free_gqa_sum_only_after_lists_without_group_items():
+    """Plan.bwd_finish_stage is VA_BWD_FINISH_HEADS (the GQA sum that reads no row flags) exactly
+    when the host-built backward list has no group items: configuration 2's list (per-head tiles),
+    not configuration 3's (group tiles), and for random lengths the stage always agrees with the
+    items' group bits."""
+    import numpy as np
+    import torch
+
+    from hackaton_amd import attention as att
+    from hackaton_amd import workloads as wl
+
+    cpu = torch.device("cpu")
+
+    def plan_of(lengths, hq, hkv):
+        offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        return att.Plan(tuple(int(x) for x in offsets), hq, hkv, cpu)
+
+    assert plan_of(wl.config_lengths(2), 12, 2).bwd_finish_stage == _lib.VA_BWD_FINISH_HEADS
+    assert plan_of(wl.config_lengths(3), 12, 2).bwd_finish_stage == _lib.VA_BWD_FINISH
+    rng = np.random.default_rng(7)
+    for _ in range(20):
+        lengths = [int(x) for x in rng.integers(1, 700, size=int(rng.integers(1, 12)))]
+        hkv = int(rng.choice([1, 2, 4]))
+        hq = hkv * int(rng.choice([1, 2, 3, 6, 7]))
+        plan = plan_of(lengths, hq, hkv)
+        items = plan.bwd_items.numpy()
+        kv = items[(items[:, 3] >> 24) == 0]
+        grouped = bool((((kv[:, 3] >> 21) & 1) == 1).any())
+        expect = _lib.VA_BWD_FINISH if grouped else _lib.VA_BWD_FINISH_HEADS
+        assert plan.bwd_finish_stage == expect
