@@ -717,16 +717,18 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
 
 // --------------------------------------------------------------------------------------------
 // dK/dV = sum over the G query heads of each key/value head of the per-head partials (fp32 sum
-// of the 16-bit partials, one rounding); 8 elements per thread.
+// of the 16-bit partials, one rounding); 8 elements per thread, 128 threads per work-group
+// (measured at config 2: 4.60 us against 4.68 with 256, 4.78 with 512, 5.14 with 1024).
 // --------------------------------------------------------------------------------------------
+constexpr int kSumThreads = 128;
 template <class E>
-__global__ __launch_bounds__(256) void bwd_gqa_sum_kernel(const uint16_t* __restrict__ dk_part,
+__global__ __launch_bounds__(kSumThreads) void bwd_gqa_sum_kernel(const uint16_t* __restrict__ dk_part,
                                                           const uint16_t* __restrict__ dv_part,
                                                           uint16_t* __restrict__ dk,
                                                           uint16_t* __restrict__ dv, long n8,
                                                           int hq, int hkv,
                                                           const uint32_t* __restrict__ flags) {
-  long i = (long)blockIdx.x * 256 + threadIdx.x;
+  long i = (long)blockIdx.x * kSumThreads + threadIdx.x;
   const uint16_t* src = dk_part;
   uint16_t* dst = dk;
   if (i >= n8) {
@@ -781,7 +783,8 @@ static hipError_t launch_bwd_finish_t(const BwdArgs& a, bool heads_only) {
   if (a.dk == nullptr || a.dk_part == a.dk) return hipSuccess;  // partials are the result
   const long n8 = a.n_tokens * a.hkv * kHeadDim / 8;
   if (n8 == 0) return hipSuccess;
-  hipLaunchKernelGGL(bwd_gqa_sum_kernel<E>, dim3((unsigned)((2 * n8 + 255) / 256)), dim3(256), 0,
+  const unsigned blocks = (unsigned)((2 * n8 + kSumThreads - 1) / kSumThreads);
+  hipLaunchKernelGGL(bwd_gqa_sum_kernel<E>, dim3(blocks), dim3(kSumThreads), 0,
                      a.stream, (const uint16_t*)a.dk_part, (const uint16_t*)a.dv_part,
                      (uint16_t*)a.dk, (uint16_t*)a.dv, n8, a.hq, a.hkv,
                      heads_only ? nullptr : a.flags);
