@@ -19,7 +19,8 @@ Also reported on the same JSON line:
   (profiles/hbm_traffic_<workload>.md);
 * by_config: the same fwd+bwd call timed at BASELINE configurations 3-5;
 * installed_path: PackedAttention (rotation, attention forward, attention backward, inverse
-  rotation with the GQA sum) as the decoder layer calls it, with host and with device lengths;
+  rotation with the GQA sum) as the decoder layer calls it, at the headline configuration (host
+  and device lengths) and at configurations 3-5 (host lengths), beside the bare kernels' time;
 * cpu_baseline: the reference's own CPU-runnable math (torch CPU scaled_dot_product_attention in
   fp32, forward + autograd backward, GQA through enable_gqa), in the two constructions the
   reference tests use, at BASELINE configuration 1 and at the headline shape.
@@ -104,7 +105,7 @@ def roofline(flops, nbytes, us, peak_tflops, peak_gbs=PEAK_HBM_GBS):
 def kernel_models(lengths, hq, hkv, elem=2):
     """Algorithmic FLOPs and bytes per launch of each kernel of one fwd+bwd call. The backward's
     bytes (dk/dv at Hkv width) belong to the pass, charged to its main kernel; a separate GQA sum
-    has no algorithmic work of its own."""
+    and the row statistics pass have no algorithmic work of their own."""
     from hackaton_amd import workloads as wl
 
     n = int(sum(lengths))
@@ -115,7 +116,13 @@ def kernel_models(lengths, hq, hkv, elem=2):
         "fwd_lean_kernel": dict(fwd),  # the many-item forward: same work
         "bwd_kernel": dict(flops=2.5 * fwd_flops, bytes=wl.backward_bytes(n, hq, hkv, elem)),
         "bwd_gqa_sum_kernel": dict(flops=0.0, bytes=0),
+        "bwd_stats_kernel": dict(flops=0.0, bytes=0),
     }
+
+
+def by_config_list(args):
+    """The other BASELINE configurations to time (--by-config)."""
+    return [int(x) for x in args.by_config.split(",") if x.strip()]
 
 
 def median_us(samples_ms, launches):
@@ -266,7 +273,10 @@ class LayerSet:
         self.dq = torch.empty_like(self.q)
         self.dk = torch.empty_like(self.k)
         self.dv = torch.empty_like(self.v)
-        self.ws, _ = att.bwd_workspace(n, hq, hkv, dev)
+        if att.bwd_workspace_needed(hq, hkv):
+            self.ws, _ = att.bwd_workspace(n, hq, hkv, dev)
+        else:  # Hq == Hkv: the kernels write dK/dV directly
+            self.ws = torch.empty(0, dtype=torch.uint8, device=dev)
         self.n = n
 
     def nbytes(self):
@@ -285,7 +295,7 @@ class Workload:
         from hackaton_amd import attention as att
         from hackaton_amd import workloads as wl
 
-        self.torch, self.lib, self._lib = torch, _lib.lib(), _lib
+        self.torch, self.lib, self._lib, self.att = torch, _lib.lib(), _lib, att
         c = wl.CONFIGS[cfg]
         self.cfg, self.c = cfg, c
         self.lengths = wl.config_lengths(cfg)
@@ -316,15 +326,15 @@ class Workload:
         argv = (s.do.data_ptr(), s.q.data_ptr(), s.k.data_ptr(), s.v.data_ptr(),
                 s.out.data_ptr(), s.lse.data_ptr(), p.bwd_items.data_ptr(), p.n_bwd, s.n,
                 self.hq, self.hkv, 128, self.scale, self.dcode, s.dq.data_ptr(), s.dk.data_ptr(),
-                s.dv.data_ptr(), s.ws.data_ptr(), s.ws.numel(), stream)
-        if stage < 0 and not self.gqa_sum_launched():  # the plan's group items write dK/dV
-            self._lib.check(self.lib.va_bwd_stage(self._lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
-        elif stage < 0:
-            self._lib.check(self.lib.va_bwd_stage(self._lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
-            self._lib.check(self.lib.va_bwd_stage(self.plan.bwd_finish_stage, *argv),
-                            "va_bwd_stage")
-        else:
-            self._lib.check(self.lib.va_bwd_stage(stage, *argv), "va_bwd_stage")
+                s.dv.data_ptr(), s.ws.data_ptr() if s.ws.numel() else None, s.ws.numel(), stream)
+        stages = self.att.bwd_stages(self.plan, True, s.ws.numel() > 0) if stage < 0 else [stage]
+        for st in stages:
+            self._lib.check(self.lib.va_bwd_stage(st, *argv), "va_bwd_stage")
+
+    def main_stage(self):
+        """The backward's main kernel stage: reading the row statistics pass's output where the
+        plan runs that pass."""
+        return self._lib.VA_BWD_MAIN_STATS if self.plan.bwd_stats else self._lib.VA_BWD_MAIN
 
     def call(self, s, stream):
         self.fwd(s, stream)
@@ -363,12 +373,17 @@ class Workload:
         """Median per-launch duration of each kernel, captured alone."""
         lib = self._lib
         out = {}
-        fwd_name = "fwd_lean_kernel" if self.plan.n_fwd >= lib.VA_FWD_MANY_ITEMS else "fwd_kernel"
+        fwd_name = "fwd_lean_kernel" if lib.fwd_many_items(sum(self.lengths), self.hq) else \
+            "fwd_kernel"
+        # the row statistics pass (where the plan runs it) before the main kernel that reads them
         for name, launch in ((fwd_name, self.fwd),
-                             ("bwd_kernel", lambda s, st: self.bwd(s, st, lib.VA_BWD_MAIN)),
+                             ("bwd_stats_kernel", lambda s, st: self.bwd(s, st, lib.VA_BWD_STATS)),
+                             ("bwd_kernel", lambda s, st: self.bwd(s, st, self.main_stage())),
                              ("bwd_gqa_sum_kernel",
                               lambda s, st: self.bwd(s, st, self.plan.bwd_finish_stage))):
             if name == "bwd_gqa_sum_kernel" and not self.gqa_sum_launched():
+                continue
+            if name == "bwd_stats_kernel" and not self.plan.bwd_stats:
                 continue
             g = self.graph(launch)
             out[name] = median_us(self.replay_ms(g, reps), len(self.sets))
@@ -402,19 +417,22 @@ def time_config(cfg, reps):
     return res
 
 
-def time_installed_path(reps):
+def time_installed_path(cfg, reps, with_device_lengths=False):
     """PackedAttention as the patched decoder layer calls it (rotation, attention forward and
-    backward, inverse rotation with the GQA sum) at the headline shape, captured in a graph with
-    its autograd backward; once with host lengths (cached host plan), once with device lengths
-    (cu_seqlens and plan built on the device in every call)."""
+    backward, inverse rotation with the GQA sum) at one configuration, captured in a graph with
+    its autograd backward; with host lengths (cached host plan) and, if asked, device lengths
+    (cu_seqlens and plan built on the device in every call). Each document is one padded batch
+    row of the decoder's input (b_idx = document, t_idx = position), as the reference's packed
+    step forms them for right-padded rows (solution/packed.py:156-172)."""
     import torch
 
     from hackaton_amd import attention as att
     from hackaton_amd import workloads as wl
 
-    c = wl.CONFIGS[2]
-    lengths = wl.config_lengths(2)
+    c = wl.CONFIGS[cfg]
+    lengths = wl.config_lengths(cfg)
     hq, hkv, n = c["hq"], c["hkv"], sum(lengths)
+    dtype = wl.torch_dtype(c["dtype"])
     dev = torch.device("cuda")
     seq = max(lengths)
     rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)],
@@ -424,19 +442,29 @@ def time_installed_path(reps):
     emb = torch.arange(seq, device=dev).float()[:, None] * inv[None]
     emb = torch.cat((emb, emb), -1)[None]
     cos, sin = emb.cos(), emb.sin()
-    n_sets = LAYER_CALLS
+    # projections and their gradient, plus what the layer keeps (rotated q/k/v, O, lse)
+    set_bytes = 2 * n * (hq + 2 * hkv) * 128 * 2 + 2 * n * hq * 128 * 2 + 4 * hq * n
+    n_sets = max(2, min(LAYER_CALLS, -(-SET_BYTES_TARGET // set_bytes)))
     sets = []
     for i in range(n_sets):
         g = torch.Generator(device=dev).manual_seed(2000 + i)
-        q = torch.randn(n, hq * 128, device=dev, generator=g).half().requires_grad_()
-        k = torch.randn(n, hkv * 128, device=dev, generator=g).half().requires_grad_()
-        v = torch.randn(n, hkv * 128, device=dev, generator=g).half().requires_grad_()
-        grad = torch.randn(n, hq * 128, device=dev, generator=g).half()
+        qk = c["qk_scale"]
+        q = (torch.randn(n, hq * 128, device=dev, generator=g) * qk).to(dtype).requires_grad_()
+        k = (torch.randn(n, hkv * 128, device=dev, generator=g) * qk).to(dtype).requires_grad_()
+        v = torch.randn(n, hkv * 128, device=dev, generator=g).to(dtype).requires_grad_()
+        grad = torch.randn(n, hq * 128, device=dev, generator=g).to(dtype)
         sets.append((q, k, v, grad))
     flops = wl.attention_flops(lengths, hq) * n_sets
-    res = {}
-    for label, lens in (("host_lengths", lengths),
-                        ("device_lengths", torch.tensor(lengths, device=dev))):
+    plan = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
+    res = {"workload": c["name"], "buffer_sets": n_sets,
+           "backward": ("per-head partials summed by the inverse rotation"
+                        if att.packed_bwd_sums_heads(plan) else
+                        "dK/dV at Hkv width from group items, then the rotation"),
+           "row_statistics_pass": bool(plan.bwd_stats)}
+    variants = [("host_lengths", lengths)]
+    if with_device_lengths:
+        variants.append(("device_lengths", torch.tensor(lengths, device=dev)))
+    for label, lens in variants:
         def step():  # gradients returned, not accumulated into .grad (no add kernels)
             for q, k, v, grad in sets:
                 out = att.packed_attention(q, k, v, cos, sin, b_idx, t_idx, seq, hq, hkv, lens,
@@ -465,9 +493,15 @@ def time_installed_path(reps):
         res[label] = {"call_us": round(ms * 1e3 / n_sets, 3),
                       "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
         del graph
-    res["note"] = ("28 layer calls per replay, fp16 projections (N, H*128), RoPE tables of "
-                   "theta 1e6; includes the rotation and its inverse, not the projections")
+    del sets
+    torch.cuda.empty_cache()
     return res
+
+
+INSTALLED_NOTE = ("layer calls over resident buffer sets per replay, projections (N, H*128) in "
+                  "the configuration's dtype, RoPE tables of theta 1e6; includes the rotation and "
+                  "its inverse, not the projections; bare_call_us is the same configuration's "
+                  "fwd+bwd kernels alone (by_config)")
 
 
 def main(argv=None):
@@ -500,8 +534,11 @@ def main(argv=None):
         stream = torch.cuda.current_stream().cuda_stream
         for s in w.sets:
             w.fwd(s, stream)
+        if w.plan.bwd_stats:
+            for s in w.sets:
+                w.bwd(s, stream, w._lib.VA_BWD_STATS)
         for s in w.sets:
-            w.bwd(s, stream, w._lib.VA_BWD_MAIN)
+            w.bwd(s, stream, w.main_stage())
         if w.gqa_sum_launched():
             for s in w.sets:
                 w.bwd(s, stream, w.plan.bwd_finish_stage)
@@ -559,7 +596,7 @@ def main(argv=None):
         "kernels_us": {k: round(v, 3) for k, v in kus.items()}}}
     del w
     torch.cuda.empty_cache()
-    for cfg_other in [int(x) for x in args.by_config.split(",") if x.strip()]:
+    for cfg_other in by_config_list(args):
         if cfg_other == args.config:
             continue
         by_config[f"config{cfg_other}"] = time_config(cfg_other, reps)
@@ -568,8 +605,15 @@ def main(argv=None):
 
     installed = None
     if not args.no_installed_path:
-        installed = time_installed_path(reps)
-        print(f"[bench] installed path: {json.dumps(installed)}", flush=True)
+        installed = {"note": INSTALLED_NOTE}
+        for cfg_i in [args.config] + [c for c in by_config_list(args) if c != args.config]:
+            r = time_installed_path(cfg_i, reps, with_device_lengths=cfg_i == args.config)
+            bare = by_config.get(f"config{cfg_i}", {}).get("call_us")
+            if bare:
+                r["bare_call_us"] = bare
+                r["over_bare"] = round(r["host_lengths"]["call_us"] / bare, 3)
+            installed[f"config{cfg_i}"] = r
+            print(f"[bench] installed path config {cfg_i}: {json.dumps(r)}", flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -15,8 +15,10 @@ VA_PLAN_FWD, VA_PLAN_BWD, VA_PLAN_BWD_HEADS, VA_PLAN_BWD_PAIRS = 0, 1, 2, 3
 VA_PLAN_BWD_GROUPS, VA_PLAN_BWD_GROUPS_ALL = 4, 5
 VA_BWD_PAIR_MIN_ITEMS = 1024
 VA_LAYOUT_PACKED, VA_LAYOUT_PADDED = 0, 1
-VA_BWD_MAIN, VA_BWD_FINISH, VA_BWD_FINISH_HEADS = 1, 2, 3
+VA_BWD_MAIN, VA_BWD_FINISH, VA_BWD_FINISH_HEADS, VA_BWD_STATS, VA_BWD_MAIN_STATS = 1, 2, 3, 4, 5
+VA_BWD_STATS_MIN_TILES = 3
 VA_FWD_MANY_ITEMS = 512
+VA_FWD_AUTO, VA_FWD_WIDE, VA_FWD_MANY = 0, 1, 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -32,6 +34,7 @@ SIGNATURES = {
     "va_head_dim": (_i32, []),
     "va_plan_size": (ctypes.c_int, [_pi32, _i32, _i32, _i32, _i32, _pi64]),
     "va_plan_build": (ctypes.c_int, [_pi32, _i32, _i32, _i32, _i32, _pi32, _i64, _pi64]),
+    "va_plan_bwd_row_stats": (ctypes.c_int, [_pi32, _i32, _pi32]),
     "va_plan_capacity": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64]),
     "va_plan_build_device": (ctypes.c_int, [_p, _i32, _i64, _i32, _i32, _i32, _p, _i64, _p]),
     "va_plan_build_device_lengths": (ctypes.c_int, [_p, _i32, _i64, _i32, _i32, _p, _i64, _p,
@@ -39,6 +42,8 @@ SIGNATURES = {
     "va_stream_capture_id": (ctypes.c_int, [_p, ctypes.POINTER(ctypes.c_uint64)]),
     "va_fwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _i32,
                               _p]),
+    "va_fwd_kernel": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
+                                     _f32, _i32, _p]),
     "va_bwd_workspace_layout": (ctypes.c_int, [_i64, _i32, _i32, _i32, _pi64, _pi64]),
     "va_bwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _f32,
                               _i32, _p, _p, _p, _p, _i64, _p]),
@@ -80,6 +85,12 @@ def lib():
             fn.argtypes = args
         _LIB = handle
     return _LIB
+
+
+def fwd_many_items(n_tokens, hq):
+    """Whether va_fwd runs its many-item kernel for these sizes (ceil(N / 128) Hq >=
+    VA_FWD_MANY_ITEMS)."""
+    return -(-int(n_tokens) // 128) * int(hq) >= VA_FWD_MANY_ITEMS
 
 
 def check(rc, what):

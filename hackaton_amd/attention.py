@@ -94,7 +94,7 @@ class Plan:
     without them."""
 
     __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "offsets", "_hq", "_hkv",
-                 "_part", "bwd_finish", "bwd_finish_stage")
+                 "_part", "bwd_finish", "bwd_finish_stage", "bwd_stats")
 
     def __init__(self, offsets, hq, hkv, device):
         cu = np.ascontiguousarray(np.asarray(offsets, dtype=np.int32))
@@ -117,6 +117,9 @@ class Plan:
         # the GQA sum of a list without group items reads no row flags (VA_BWD_FINISH_HEADS)
         self.bwd_finish_stage = _lib.VA_BWD_FINISH if bool(grouped.any()) else \
             _lib.VA_BWD_FINISH_HEADS
+        # the backward's row statistics in a pass of their own where the documents are long
+        # enough for it to pay (va_plan_bwd_row_stats)
+        self.bwd_stats = bwd_row_stats(cu)
 
     def partial_bwd(self):
         """(items, n) of the backward list without group items (built on first use)."""
@@ -125,6 +128,17 @@ class Plan:
             host = build_plan_host(cu, self._hq, self._hkv, _lib.VA_PLAN_BWD)
             self._part = (torch.from_numpy(host).to(self.bwd_items.device), host.shape[0])
         return self._part
+
+
+def bwd_row_stats(cu):
+    """Whether the backward's row statistics {lse log2 e, rowsum(dO * O)} pay for a pass of their
+    own over these documents (the C planner's rule: on average VA_BWD_STATS_MIN_TILES or more
+    128-key tiles cover each query row)."""
+    cu = np.ascontiguousarray(np.asarray(cu, dtype=np.int32))
+    use = np.zeros(1, dtype=np.int32)
+    check(lib().va_plan_bwd_row_stats(cu.ctypes.data_as(_lib._pi32), cu.shape[0] - 1,
+                                      use.ctypes.data_as(_lib._pi32)), "va_plan_bwd_row_stats")
+    return bool(use[0])
 
 
 def build_plan_host(cu, hq, hkv, kind):
@@ -151,7 +165,7 @@ class DevicePlan:
     sizes bound; its slots past the real items are empty items that the kernels skip."""
 
     __slots__ = ("fwd_items", "n_fwd", "bwd_items", "n_bwd", "total", "cu", "_part",
-                 "bwd_finish", "bwd_finish_stage", "__weakref__")
+                 "bwd_finish", "bwd_finish_stage", "bwd_stats", "__weakref__")
 
     def __init__(self, lengths, n_tokens, hq, hkv):
         lengths = lengths.reshape(-1)
@@ -179,6 +193,7 @@ class DevicePlan:
         self.bwd_items = part
         self.bwd_finish = hq > hkv  # the device list's group tiles are not known here
         self.bwd_finish_stage = _lib.VA_BWD_FINISH
+        self.bwd_stats = False  # the document lengths are not known on the host
         if hq > hkv and n_docs > 0:
             self.bwd_items = torch.empty_like(part)
             check(lib().va_plan_build_device(self.cu.data_ptr(), n_docs, n_tokens, hq, hkv,
@@ -257,14 +272,33 @@ def attention_forward(query, key, value, plan, scale):
     return out, lse
 
 
+def bwd_workspace_needed(hq, hkv, outputs=True):
+    """Whether the backward needs its workspace (per-query-head dK/dV partials, row flags and row
+    statistics): not when Hq == Hkv and dK/dV are returned, which the kernels then write directly
+    (the reference's expanded-K/V call, solution/attention.py:230-232)."""
+    return hq != hkv or not outputs
+
+
 def bwd_workspace(n, hq, hkv, device):
-    """Workspace of the backward (per-query-head dK/dV partials) and its byte offsets."""
+    """Workspace of the backward (per-query-head dK/dV partials, row flags, row statistics) and
+    the byte offsets of the two partial arrays."""
     offsets = np.zeros(2, dtype=np.int64)
     nbytes = np.zeros(1, dtype=np.int64)
     check(lib().va_bwd_workspace_layout(n, hq, hkv, HEAD_DIM, offsets.ctypes.data_as(_lib._pi64),
                                         nbytes.ctypes.data_as(_lib._pi64)),
           "va_bwd_workspace_layout")
     return torch.empty(int(nbytes[0]), dtype=torch.uint8, device=device), [int(x) for x in offsets]
+
+
+def bwd_stages(plan, outputs=True, workspace=True):
+    """The va_bwd_stage calls of one backward over `plan`: the row-statistics pass where the plan
+    says it pays (it needs the workspace), the main kernel, and the GQA sum unless the plan's group
+    items wrote every dK/dV row, Hq == Hkv, or the per-head partials are the result."""
+    stats = workspace and getattr(plan, "bwd_stats", False)
+    stages = [_lib.VA_BWD_STATS, _lib.VA_BWD_MAIN_STATS] if stats else [_lib.VA_BWD_MAIN]
+    if outputs and getattr(plan, "bwd_finish", True):
+        stages.append(getattr(plan, "bwd_finish_stage", _lib.VA_BWD_FINISH))
+    return stages
 
 
 def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=True):
@@ -283,18 +317,17 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
         dk, dv = torch.empty_like(key), torch.empty_like(value)
     else:
         dk = dv = None
-    ws, offs = bwd_workspace(n, hq, hkv, query.device)
+    if bwd_workspace_needed(hq, hkv, outputs):
+        ws, offs = bwd_workspace(n, hq, hkv, query.device)
+    else:
+        ws, offs = None, None
     items, n_items = (plan.bwd_items, plan.n_bwd) if outputs else plan.partial_bwd()
     argv = (_ptr(grad), _ptr(query), _ptr(key), _ptr(value), _ptr(out), _ptr(lse),
             _ptr(items), n_items, n, hq, hkv, d, float(scale), dtype,
-            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws) if ws.numel() else None, ws.numel(), _stream())
-    if outputs and not getattr(plan, "bwd_finish", True):  # group items wrote every dK/dV row
-        check(lib().va_bwd_stage(_lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
-    elif outputs and getattr(plan, "bwd_finish_stage", None) == _lib.VA_BWD_FINISH_HEADS:
-        check(lib().va_bwd_stage(_lib.VA_BWD_MAIN, *argv), "va_bwd_stage")
-        check(lib().va_bwd_stage(_lib.VA_BWD_FINISH_HEADS, *argv), "va_bwd_stage")
-    else:
-        check(lib().va_bwd(*argv), "va_bwd")
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() if ws is not None else 0,
+            _stream())
+    for stage in bwd_stages(plan, outputs, ws is not None):
+        check(lib().va_bwd_stage(stage, *argv), "va_bwd_stage")
     if outputs:
         return dq, dk, dv
     part = n * hq * d * 2
@@ -480,12 +513,22 @@ def set_save_policy(policy):
     SAVE_POLICY = policy
 
 
+def packed_bwd_sums_heads(plan):
+    """Whether PackedAttention's backward leaves per-query-head dK/dV partials for the inverse
+    rotation to sum (one pass over them instead of a GQA sum and a rotation): where the plan's
+    backward would launch its GQA sum. Where it would not (every key tile in group items that
+    cover the whole GQA group, or Hq == Hkv), the main kernel writes dK/dV at Hkv width and the
+    rotation reads those."""
+    return bool(getattr(plan, "bwd_finish", True))
+
+
 class PackedAttention(torch.autograd.Function):
     """Autograd node of the decoder layer's call: rotary embedding, then causal attention of every
     document of the packed rows; returns (N, heads * D) in the compute type.
 
-    The backward runs the attention backward kernels (dK/dV summed over each GQA group in fp32)
-    and the inverse rotation straight from the fp32 accumulators. What is kept for it follows
+    The backward runs the attention backward kernels and the inverse rotation: the rotation sums
+    per-query-head dK/dV partials over each GQA group in fp32, or, where the plan's group items
+    write dK/dV at Hkv width (packed_bwd_sums_heads), rotates those. What is kept for it follows
     SAVE_POLICY: the rotated operands, O and lse ("outputs"), or only the three projections,
     recomputing the rotation and the forward like solution/attention.py:250-279 ("inputs", and
     always when `offload` moves them to pinned host memory). Returns the three projection
@@ -522,13 +565,17 @@ class PackedAttention(torch.autograd.Function):
             q, k, v = OFFLOADER.load(ctx.item) if hasattr(ctx, "item") else ctx.saved_tensors
             out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
                                                    kv_heads, lengths, scale)
-        # dq and the per-query-head dK/dV partials; the inverse rotation sums the partials over
-        # each GQA group (as solution/attention.py:113-134 sums its expanded copies)
-        dq_r, dk_part, dv_part, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
-                                                         outputs=False)
+        if packed_bwd_sums_heads(plan):
+            # dq and the per-query-head dK/dV partials; the inverse rotation sums the partials
+            # over each GQA group (as solution/attention.py:113-134 sums its expanded copies)
+            dq_r, dk_r, dv_r, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
+                                                       outputs=False)
+        else:
+            # the plan's group items (or Hq == Hkv) write dK/dV at Hkv width themselves
+            dq_r, dk_r, dv_r = attention_backward(dout, qr, kr, vr, out, lse, plan, scale)
         q_dtype, k_dtype, v_dtype = ctx.dtypes
-        dq, dk, dv = rope_backward(dq_r, dk_part, dv_part, cos, sin, b_idx, t_idx, heads,
-                                   kv_heads, q_dtype, expand=True)
+        dq, dk, dv = rope_backward(dq_r, dk_r, dv_r, cos, sin, b_idx, t_idx, heads, kv_heads,
+                                   q_dtype, expand=packed_bwd_sums_heads(plan))
         grads = (dq, dk.to(k_dtype), dv.to(v_dtype))
         return (*grads, None, None, None, None, None, None, None, None, None, None)
 

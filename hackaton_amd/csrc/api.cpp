@@ -63,6 +63,7 @@ int check_ptrs(std::initializer_list<const void*> ptrs, const char* what) {
 
 int64_t round256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
+
 }  // namespace
 
 extern "C" const char* va_last_error(void) { return va::last_error_buffer(); }
@@ -72,6 +73,16 @@ extern "C" int32_t va_head_dim(void) { return va::kHeadDim; }
 extern "C" int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
                       const int32_t* items, int64_t n_items, int64_t total_tokens, int32_t hq,
                       int32_t hkv, int32_t head_dim, float scale, int32_t dtype, void* stream) {
+  return va_fwd_kernel(VA_FWD_AUTO, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
+                       head_dim, scale, dtype, stream);
+}
+
+extern "C" int va_fwd_kernel(int32_t kernel, const void* q, const void* k, const void* v,
+                             void* out, float* lse, const int32_t* items, int64_t n_items,
+                             int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim,
+                             float scale, int32_t dtype, void* stream) {
+  if (kernel != VA_FWD_AUTO && kernel != VA_FWD_WIDE && kernel != VA_FWD_MANY)
+    return va::fail(VA_EINVAL, "va_fwd_kernel: kernel %d", kernel);
   int rc = check_attn_shape(total_tokens, hq, hkv, head_dim);
   if (rc) return rc;
   if ((rc = check_dtype16(dtype))) return rc;
@@ -80,8 +91,12 @@ extern "C" int va_fwd(const void* q, const void* k, const void* v, void* out, fl
     return va::fail(VA_EINVAL, "scale must be finite and positive");
   if (n_items == 0 || total_tokens == 0) return VA_OK;
   if ((rc = check_ptrs({q, k, v, out, lse, items}, "va_fwd"))) return rc;
+  if (kernel == VA_FWD_AUTO)
+    kernel = (total_tokens + va::kFwdBlockM - 1) / va::kFwdBlockM * hq >= VA_FWD_MANY_ITEMS
+                 ? VA_FWD_MANY
+                 : VA_FWD_WIDE;
   va::FwdArgs a{q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, scale, dtype,
-                (hipStream_t)stream};
+                (hipStream_t)stream, kernel};
   hipError_t e = va::launch_fwd(a);
   return e == hipSuccess ? VA_OK : hip_fail(e, "va_fwd launch");
 }
@@ -94,8 +109,9 @@ extern "C" int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t
   const int64_t part = round256(total_tokens * hq * head_dim * 2);
   offsets[0] = 0;     // per-query-head dK partials (N, Hq, D), element type
   offsets[1] = part;  // per-query-head dV partials
-  // then (N) uint32 row flags at 2 part: which rows a GQA group item finished itself
-  *bytes = 2 * part + round256(total_tokens * 4);
+  // then (N) uint32 row flags at 2 part: which rows a GQA group item finished itself; then
+  // (Hq, N) x 2 fp32 row statistics {lse log2 e, rowsum(dO * O)} of the row-statistics pass
+  *bytes = 2 * part + round256(total_tokens * 4) + round256(total_tokens * hq * 8);
   return VA_OK;
 }
 
@@ -130,9 +146,19 @@ int bwd_checked(int32_t stage, const void* dout, const void* q, const void* k, c
   void* dk_part = direct ? dk : static_cast<void*>(ws + offs[0]);
   void* dv_part = direct ? dv : static_cast<void*>(ws + offs[1]);
   uint32_t* flags = direct ? nullptr : reinterpret_cast<uint32_t*>(ws + 2 * offs[1]);
+  // The row statistics exist for the stages that write or read them (they need the workspace).
+  const bool with_stats = stage == VA_BWD_STATS || stage == VA_BWD_MAIN_STATS;
+  if (with_stats && direct && (rc = check_ptrs({workspace}, "va_bwd workspace (statistics)")))
+    return rc;
+  if (with_stats && direct && workspace_bytes < need)
+    return va::fail(VA_ECAPACITY, "workspace %lld bytes, the row statistics need %lld",
+                    (long long)workspace_bytes, (long long)need);
+  float* stats = with_stats ? reinterpret_cast<float*>(ws + 2 * offs[1] + round256(total_tokens * 4))
+                            : nullptr;
   va::BwdArgs a{dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, scale, dtype,
-                dq, dk_part, dv_part, dk, dv, flags, (hipStream_t)stream};
-  hipError_t e = stage < 0 ? va::launch_bwd(a) : va::launch_bwd_stage(a, stage);
+                dq, dk_part, dv_part, dk, dv, flags, stats, (hipStream_t)stream};
+  const int kstage = stage == VA_BWD_MAIN_STATS ? 1 : stage == VA_BWD_STATS ? 4 : stage;
+  hipError_t e = stage < 0 ? va::launch_bwd(a) : va::launch_bwd_stage(a, kstage);
   return e == hipSuccess ? VA_OK : hip_fail(e, "va_bwd launch");
 }
 
@@ -153,7 +179,8 @@ extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, cons
                             int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype,
                             void* dq, void* dk, void* dv, void* workspace,
                             int64_t workspace_bytes, void* stream) {
-  if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH && stage != VA_BWD_FINISH_HEADS)
+  if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH && stage != VA_BWD_FINISH_HEADS &&
+      stage != VA_BWD_STATS && stage != VA_BWD_MAIN_STATS)
     return va::fail(VA_EINVAL, "va_bwd_stage: stage %d", stage);
   return va::bwd_checked(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
                          head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);

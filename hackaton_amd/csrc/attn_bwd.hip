@@ -70,7 +70,7 @@ __device__ __host__ constexpr int block_c(int b, int /*i*/) { return b; }
 // SHAPE (item word bits 20-21): 0 per head, 1 pair, 2 group; a template constant, so that each
 // shape's step loop carries no unit / head arithmetic of the others (per-head items: no division
 // by the step count, no pair selects).
-template <class E, int SHAPE>
+template <class E, int SHAPE, bool PREP>
 __device__ __forceinline__ void bwd_kv_item(
     lds_u16* smem, float (&stat)[2][2][2][bwd::BQ], const int4 it,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -78,7 +78,7 @@ __device__ __forceinline__ void bwd_kv_item(
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part, uint16_t* __restrict__ dk_out,
     uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags, int n_tokens, int hq, int hkv,
-    float scale, float scale_log2) {
+    float scale, float scale_log2, const f32x2* __restrict__ stats) {
   using namespace bwd;
   const int k0 = it.x, doc_end = it.y, h = it.w & kHeadMask;
   constexpr bool pair = SHAPE == 1;
@@ -160,29 +160,32 @@ __device__ __forceinline__ void bwd_kv_item(
   // loads are then complete and the dot product does not stall the step.
   const int s_row = tid >> 4, s_col = 8 * (tid & 15);
   const int s_voff = (s_row * (int)qrow + s_col) * 2;  // from the unit's (first row, head)
-  u32x4 sreg[4], oreg[2];
+  u32x4 sreg[4], oreg[PREP ? 1 : 2];
   float st_lse = 0.f;
+  f32x2 st_pre = f32x2{0.f, 0.f};
   int st_row = 0;
   auto gload_pair = [&](int p) {
     int row0[2];
-    const float* lrow[2];
+    long lrow[2];
 #pragma unroll
     for (int sh = 0; sh < 2; ++sh) {
       // The unit's head column is in the descriptor's base (wave-uniform), so the per-lane offset
       // is the same for every unit.
       const int hs = head_of(p, sh);
       row0[sh] = k0 + min(step_of(p, sh), n_steps - 1) * BQ;
-      lrow[sh] = lse + (long)hs * n_tokens;
+      lrow[sh] = (long)hs * n_tokens;
       const long base = (long)row0[sh] * qrow + (long)hs * D;
       const long bytes = ((long)(doc_end - row0[sh] - 1) * qrow + D) * 2;
       sreg[2 * sh] = bload16(make_rsrc(q + base, bytes), s_voff);
       sreg[2 * sh + 1] = bload16(make_rsrc(dout + base, bytes), s_voff);
-      oreg[sh] = bload16(make_rsrc(out + base, bytes), s_voff);
+      if constexpr (!PREP) oreg[sh] = bload16(make_rsrc(out + base, bytes), s_voff);
     }
     if (tid < 64) {  // raw value: scaled at the store, so that no wait follows the loads here
       const int sh = tid >> 5;
       st_row = (sh ? row0[1] : row0[0]) + (tid & 31);
-      st_lse = (sh ? lrow[1] : lrow[0])[min(st_row, doc_end - 1)];
+      const long at = (sh ? lrow[1] : lrow[0]) + min(st_row, doc_end - 1);
+      if constexpr (PREP) st_pre = stats[at];
+      else st_lse = lse[at];
     }
   };
   auto store_pair = [&](int stage) {
@@ -191,15 +194,24 @@ __device__ __forceinline__ void bwd_kv_item(
       st128(smem + ((i & 1) ? KV_OFF_DO : KV_OFF_Q) + (stage * 2 + (i >> 1)) * ROWT +
                 s_row * LD + s_col,
             sreg[i]);
+    if constexpr (PREP) {  // lse log2 e and delta from the row-statistics pass
+      if (tid < 64) {
+        const bool in = st_row < doc_end;
+        stat[stage][0][tid >> 5][tid & 31] = in ? st_pre[0] : INFINITY;
+        stat[stage][1][tid >> 5][tid & 31] = in ? st_pre[1] : 0.f;
+      }
+    } else {
 #pragma unroll
-    for (int sh = 0; sh < 2; ++sh) {  // delta: sum over the 16 threads that share a row
-      float d = 0.f;
+      for (int sh = 0; sh < 2; ++sh) {  // delta: sum over the 16 threads that share a row
+        float d = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) d = E::dot2(oreg[sh][w], sreg[2 * sh + 1][w], d);
-      d = sum_rows16(d);
-      if ((tid & 15) == 0) stat[stage][1][sh][s_row] = d;
+        for (int w = 0; w < 4; ++w) d = E::dot2(oreg[sh][w], sreg[2 * sh + 1][w], d);
+        d = sum_rows16(d);
+        if ((tid & 15) == 0) stat[stage][1][sh][s_row] = d;
+      }
+      if (tid < 64)
+        stat[stage][0][tid >> 5][tid & 31] = st_row < doc_end ? st_lse * kLog2e : INFINITY;
     }
-    if (tid < 64) stat[stage][0][tid >> 5][tid & 31] = st_row < doc_end ? st_lse * kLog2e : INFINITY;
   };
 
   const int rm_read = perm32(l32) * LD + 8 * hi;                 // A rows = queries
@@ -372,8 +384,10 @@ __device__ __forceinline__ void bwd_kv_item(
   };
   // The GQA sum reads how many heads each partial of a row sums (S; G: a group item wrote the
   // row's dK/dV itself): every key row belongs to one tile, whose items of the GQA group's first
-  // head write its flag.
-  if (flags != nullptr && h % G == 0 && tid < BK && k0 + tid < doc_end) flags[k0 + tid] = S;
+  // head write its flag. Without outputs every head's partial holds a share (zeros beside a
+  // group item's sum, below): 1, so that any later sum adds all G.
+  if (flags != nullptr && h % G == 0 && tid < BK && k0 + tid < doc_end)
+    flags[k0 + tid] = dk_out != nullptr ? S : 1;
   if constexpr (pair) {
     // Each half holds the whole dK/dV of its head: both go out through this wave's own row tile
     // (the LDS stages are free after the loop's last barrier), dK scaled.
@@ -406,12 +420,25 @@ __device__ __forceinline__ void bwd_kv_item(
     store(dvacc, 1.f, dv_part);
     return;
   }
-  if (S == G) {
+  if (S == G && dk_out != nullptr) {
     if (half) finish(dvacc, dkacc, 1.f, dv_out, hkv, kvh);
     else finish(dkacc, dvacc, scale, dk_out, hkv, kvh);
   } else {
     if (half) finish(dvacc, dkacc, 1.f, dv_part, hq, h);
     else finish(dkacc, dvacc, scale, dk_part, hq, h);
+    if constexpr (grouped) {
+      // No outputs: the caller sums all G per-head partials of each row, so the item's other
+      // heads' partials hold zeros (its sum went into head h's), and that sum is exact.
+      if (dk_out == nullptr) {
+        uint16_t* part = half ? dv_part : dk_part;
+        for (int x = 1; x < S; ++x)
+          for (int i = lane; i < 32 * (D / 8); i += 64) {
+            const int r = i / (D / 8), c = i % (D / 8);
+            if (kw0 + r < doc_end)
+              gstore16(part + ((long)(kw0 + r) * hq + h + x) * D + 8 * c, u32x4{0u, 0u, 0u, 0u});
+          }
+      }
+    }
   }
 }
 
@@ -420,13 +447,13 @@ __device__ __forceinline__ void bwd_kv_item(
 // one GQA group: then half j takes head h + j over both tiles of every pair, so the halves share
 // the K/V tiles, never exchange dQ, and each writes all 128 columns of its head.
 // --------------------------------------------------------------------------------------------
-template <class E, bool PAIR>
+template <class E, bool PAIR, bool PREP>
 __device__ __forceinline__ void bwd_q_item(
     lds_u16* smem, const int4 it, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, uint16_t* __restrict__ dq, int n_tokens, int hq, int hkv,
-    float scale, float scale_log2, float* stat_f) {
+    float scale, float scale_log2, float* stat_f, const f32x2* __restrict__ stats) {
   using namespace bwd;
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kHeadMask;
   constexpr bool pair = PAIR;
@@ -476,25 +503,35 @@ __device__ __forceinline__ void bwd_q_item(
     const brsrc rq = make_rsrc(q + (long)q0 * qrow, bytes);
     const brsrc rd = make_rsrc(dout + (long)q0 * qrow, bytes);
     const brsrc ro = make_rsrc(out + (long)q0 * qrow, bytes);
-    u32x4 xq[QB / 32], xd[QB / 32], xo[QB / 32];
+    u32x4 xq[QB / 32], xd[QB / 32], xo[PREP ? 1 : QB / 32];
 #pragma unroll
     for (int i = 0; i < QB / 32; ++i) {
       const int off = ((srow + 32 * i) * (int)qrow + hh * D + scol) * 2;
       xq[i] = bload16(rq, off);
       xd[i] = bload16(rd, off);
-      xo[i] = bload16(ro, off);
+      if constexpr (!PREP) xo[i] = bload16(ro, off);
     }
-    if (tid < QB)
+    if constexpr (PREP) {  // lse log2 e and delta from the row-statistics pass
+      if (tid < QB) {
+        const bool in = q0 + tid < doc_end;
+        const f32x2 x = stats[(long)hh * n_tokens + min(q0 + tid, doc_end - 1)];
+        st[tid] = in ? x[0] : INFINITY;
+        st[QB + tid] = in ? x[1] : 0.f;
+      }
+    } else if (tid < QB) {
       st[tid] = q0 + tid < doc_end ? lse[(long)hh * n_tokens + q0 + tid] * kLog2e : INFINITY;
+    }
 #pragma unroll
     for (int i = 0; i < QB / 32; ++i) {
       st128(smem + off_q + (srow + 32 * i) * LD + scol, xq[i]);
       st128(smem + off_q + QB * LD + (srow + 32 * i) * LD + scol, xd[i]);
-      float d = 0.f;
+      if constexpr (!PREP) {
+        float d = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) d = E::dot2(xo[i][w], xd[i][w], d);
-      d = sum_rows16(d);
-      if ((tid & 15) == 0) st[QB + srow + 32 * i] = d;
+        for (int w = 0; w < 4; ++w) d = E::dot2(xo[i][w], xd[i][w], d);
+        d = sum_rows16(d);
+        if ((tid & 15) == 0) st[QB + srow + 32 * i] = d;
+      }
     }
   };
   stage_head(h, QT_OFF, stat_f);
@@ -667,7 +704,9 @@ __device__ __forceinline__ void bwd_q_item(
   else finish(std::integral_constant<int, 0>{});
 }
 
-template <class E>
+// PREP: lse log2 e and delta come from the row-statistics pass (`stats`); otherwise the items
+// load O beside dO and form delta themselves.
+template <class E, bool PREP>
 // Arguments in the order the work-group needs them: the first 14 dwords are preloaded into
 // SGPRs at launch (-amdgpu-kernarg-preload-count), so the work item's load starts at once.
 __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
@@ -676,7 +715,8 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, int hq, int hkv,
     const float* __restrict__ lse, uint16_t* __restrict__ dq, uint16_t* __restrict__ dk_part,
     uint16_t* __restrict__ dv_part, int n_tokens, float scale, float scale_log2,
-    uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags) {
+    uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags,
+    const f32x2* __restrict__ stats) {
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
   __shared__ __attribute__((aligned(16))) float qstat[4 * bwd::QB];  // q items: [head][lse|del]
@@ -686,32 +726,68 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
   // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
   const int kind = it.w >> 24, h = it.w & bwd::kHeadMask, shape = (it.w >> 20) & 15;
   // Pair items (shape 1) take heads h, h + 1 of one GQA group; group items (shape 2, kv only)
-  // heads h .. h + S - 1 (S >= 2 dividing G, h a multiple of S), and with S = G need the Hkv-wide
-  // outputs.
+  // heads h .. h + S - 1 (S >= 2 dividing G, h a multiple of S).
   const int G = hq / hkv, S = ((it.w >> kItemHeadsShift) & 0xff) + 1;
   if (it.x >= it.y || it.z < 0 || it.x < it.z || it.y > n_tokens || h >= hq ||
       (kind != bwd::kKindKV && kind != bwd::kKindQ) || shape > 2 ||
       (shape < 2 && S != 1) ||
       (shape == 1 && (h + 1 >= hq || h / G != (h + 1) / G)) ||
-      (shape == 2 && (kind != bwd::kKindKV || S < 2 || G % S != 0 || h % S != 0 ||
-                      (S == G && dk_out == nullptr))))
+      (shape == 2 && (kind != bwd::kKindKV || S < 2 || G % S != 0 || h % S != 0)))
     return;
   if (kind == bwd::kKindKV) {
     if (shape == 0)
-      bwd_kv_item<E, 0>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
-                        dv_out, flags, n_tokens, hq, hkv, scale, scale_log2);
+      bwd_kv_item<E, 0, PREP>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats);
     else if (shape == 1)
-      bwd_kv_item<E, 1>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
-                        dv_out, flags, n_tokens, hq, hkv, scale, scale_log2);
+      bwd_kv_item<E, 1, PREP>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats);
     else
-      bwd_kv_item<E, 2>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
-                        dv_out, flags, n_tokens, hq, hkv, scale, scale_log2);
+      bwd_kv_item<E, 2, PREP>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats);
   } else if (shape == 0) {
-    bwd_q_item<E, false>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
-                         scale_log2, qstat);
+    bwd_q_item<E, false, PREP>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
+                               scale_log2, qstat, stats);
   } else {
-    bwd_q_item<E, true>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
-                        scale_log2, qstat);
+    bwd_q_item<E, true, PREP>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
+                              scale_log2, qstat, stats);
+  }
+}
+
+// --------------------------------------------------------------------------------------------
+// Row statistics of the backward, once per (query head, row): {lse log2 e, delta = rowsum(dO * O)}
+// in fp32, with the arithmetic of the items' own staging (16 threads per row, v_dot2 over each
+// thread's 8 elements, then the 16-lane DPP sum), so that the main kernel's results do not depend
+// on where delta was formed. Work-group: 64 rows of one head, 4 rows per thread (8 loads in
+// flight each). Rows past n_tokens are not touched.
+// --------------------------------------------------------------------------------------------
+constexpr int kStatThreads = 256, kStatRows = 64;
+template <class E>
+__global__ __launch_bounds__(kStatThreads) void bwd_stats_kernel(
+    const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
+    const float* __restrict__ lse, f32x2* __restrict__ stats, int n_tokens, int hq) {
+  const int h = blockIdx.y, tid = threadIdx.x;
+  const int r0 = blockIdx.x * kStatRows + (tid >> 4), col = 8 * (tid & 15);
+  const long qrow = (long)hq * kHeadDim;
+  constexpr int R = kStatRows / (kStatThreads / 16);
+  u32x4 o[R], g[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int r = min(r0 + 16 * i, n_tokens - 1);
+    const long at = r * qrow + (long)h * kHeadDim + col;
+    o[i] = gload16(out + at);
+    g[i] = gload16(dout + at);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float d = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) d = E::dot2(o[i][w], g[i][w], d);
+    d = sum_rows16(d);
+    const int r = r0 + 16 * i;
+    if ((tid & 15) == 0 && r < n_tokens) {
+      const long at = (long)h * n_tokens + r;
+      stats[at] = f32x2{lse[at] * kLog2e, d};
+    }
   }
 }
 
@@ -766,14 +842,25 @@ __global__ __launch_bounds__(kSumThreads) void bwd_gqa_sum_kernel(const uint16_t
 }
 
 template <class E>
+static hipError_t launch_bwd_stats_t(const BwdArgs& a) {
+  if (a.n_tokens == 0 || a.stats == nullptr) return hipSuccess;
+  const dim3 grid((unsigned)((a.n_tokens + kStatRows - 1) / kStatRows), (unsigned)a.hq);
+  hipLaunchKernelGGL(bwd_stats_kernel<E>, grid, dim3(kStatThreads), 0, a.stream,
+                     (const uint16_t*)a.out, (const uint16_t*)a.dout, a.lse, (f32x2*)a.stats,
+                     (int)a.n_tokens, a.hq);
+  return hipGetLastError();
+}
+
+// PREP: the row statistics are in a.stats already (written by launch_bwd_stats_t).
+template <class E, bool PREP>
 static hipError_t launch_bwd_main_t(const BwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
-  hipLaunchKernelGGL((bwd_kernel<E>), dim3((unsigned)a.n_items), dim3(bwd::NT), 0, a.stream,
-                     (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
+  hipLaunchKernelGGL((bwd_kernel<E, PREP>), dim3((unsigned)a.n_items), dim3(bwd::NT), 0,
+                     a.stream, (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.out, (const uint16_t*)a.dout, a.hq,
                      a.hkv, a.lse, (uint16_t*)a.dq, (uint16_t*)a.dk_part, (uint16_t*)a.dv_part,
                      (int)a.n_tokens, a.scale, a.scale * kLog2e, (uint16_t*)a.dk,
-                     (uint16_t*)a.dv, a.flags);
+                     (uint16_t*)a.dv, a.flags, (const f32x2*)a.stats);
   return hipGetLastError();
 }
 
@@ -793,7 +880,12 @@ static hipError_t launch_bwd_finish_t(const BwdArgs& a, bool heads_only) {
 
 hipError_t launch_bwd_stage(const BwdArgs& a, int stage) {
   const bool bf = a.dtype != 0;
-  if (stage == 1) return bf ? launch_bwd_main_t<BF16>(a) : launch_bwd_main_t<F16>(a);
+  if (stage == 4) return bf ? launch_bwd_stats_t<BF16>(a) : launch_bwd_stats_t<F16>(a);
+  if (stage == 1) {
+    if (a.stats != nullptr)
+      return bf ? launch_bwd_main_t<BF16, true>(a) : launch_bwd_main_t<F16, true>(a);
+    return bf ? launch_bwd_main_t<BF16, false>(a) : launch_bwd_main_t<F16, false>(a);
+  }
   const bool heads_only = stage == 3;
   return bf ? launch_bwd_finish_t<BF16>(a, heads_only) : launch_bwd_finish_t<F16>(a, heads_only);
 }

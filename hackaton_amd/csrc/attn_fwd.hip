@@ -585,7 +585,7 @@ __global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
 template <class E>
 static hipError_t launch_fwd_t(const FwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
-  if (a.n_items >= kFwdLeanMinItems) {
+  if (a.kernel == 2) {
     hipLaunchKernelGGL((fwd_lean_kernel<E>), dim3((unsigned)a.n_items), dim3(fwdl::NT), 0,
                        a.stream, (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
                        (const uint16_t*)a.v, a.hq, a.hkv, (uint16_t*)a.out, a.lse,

@@ -22,8 +22,9 @@
 
 namespace {
 
-// The partials of N * Hq <= 131072 rows at head_dim 128 (64 MiB) and the row flags (4 N bytes).
-constexpr int64_t kNoAllocScratchBytes = int64_t(65) << 20;
+// The partials of N * Hq <= 131072 rows at head_dim 128 (64 MiB), the row flags (4 N bytes) and
+// the row statistics (8 N Hq bytes).
+constexpr int64_t kNoAllocScratchBytes = int64_t(66) << 20;
 constexpr int kMaxDevices = 64;
 
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];

@@ -52,10 +52,19 @@ bool is_group_kind(int32_t kind) {
 }
 int32_t item_head(int32_t d) { return d & va::kItemHeadMask; }
 
+// 128-row tiles of the documents (sum of ceil(length / 128); empty documents have none).
+int64_t doc_tiles(const int32_t* cu, int32_t n_docs) {
+  int64_t t = 0;
+  for (int32_t i = 0; i < n_docs; ++i)
+    if (cu[i + 1] > cu[i]) t += ((int64_t)cu[i + 1] - cu[i] + va::kBwdBlockN - 1) / va::kBwdBlockN;
+  return t;
+}
+
 std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv,
                              int32_t kind) {
   std::vector<Item> items;
-  const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
+  const bool pairs =
+      kind != VA_PLAN_FWD && va::bwd_plan_pairs(doc_tiles(cu, n_docs), hq, hkv, kind);
   const int32_t group = hq / hkv, rows = pairs ? (group + 1) / 2 : group;
   // Group plans: the largest group-item work that keeps the plan about as long as its VA_PLAN_BWD
   // form: that list's longest item, or its work per CU when that is more (measured at configs
@@ -171,7 +180,8 @@ std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
 int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind) {
   if (is_group_kind(kind)) return (int64_t)make_items(cu, n_docs, hq, hkv, kind).size();
   int64_t n = 0;
-  const bool pairs = kind != VA_PLAN_FWD && va::bwd_plan_pairs(cu[n_docs], n_docs, hq, hkv, kind);
+  const bool pairs =
+      kind != VA_PLAN_FWD && va::bwd_plan_pairs(doc_tiles(cu, n_docs), hq, hkv, kind);
   const int64_t kv_per_tile = pairs ? (int64_t)hkv * ((hq / hkv + 1) / 2) : hq;  // per kind
   for (int32_t i = 0; i < n_docs; ++i) {
     const int64_t len = (int64_t)cu[i + 1] - cu[i];
@@ -219,6 +229,22 @@ extern "C" int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t 
   return VA_OK;
 }
 
+extern "C" int va_plan_bwd_row_stats(const int32_t* cu_seqlens, int32_t n_docs, int32_t* use) {
+  int rc = check_cu(cu_seqlens, n_docs);
+  if (rc) return rc;
+  if (use == nullptr) return va::fail(VA_EINVAL, "va_plan_bwd_row_stats: NULL output");
+  // sum over rows of the number of 128-key tiles at or before the row's tile
+  int64_t rows = 0, covered = 0;
+  for (int32_t i = 0; i < n_docs; ++i) {
+    const int64_t len = (int64_t)cu_seqlens[i + 1] - cu_seqlens[i];
+    const int64_t full = len / va::kBwdBlockN, rest = len % va::kBwdBlockN;
+    covered += (int64_t)va::kBwdBlockN * full * (full + 1) / 2 + rest * (full + 1);
+    rows += len;
+  }
+  *use = rows > 0 && covered >= (int64_t)VA_BWD_STATS_MIN_TILES * rows;
+  return VA_OK;
+}
+
 extern "C" int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t kind,
                                 int64_t* capacity) {
   if (capacity == nullptr) return va::fail(VA_EINVAL, "capacity is NULL");
@@ -261,8 +287,7 @@ extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_
   const bool fwd = kind == VA_PLAN_FWD;
   const hipError_t e = va::launch_plan_device(
       cu_seqlens_device, nullptr, n_docs, (int)n_tokens, hq, hkv, fwd ? items_device : nullptr,
-      capacity, fwd ? nullptr : items_device, capacity,
-      !fwd && va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, kind),
+      capacity, fwd ? nullptr : items_device, capacity, kind,
       kind == VA_PLAN_BWD_GROUPS ? 1 : (kind == VA_PLAN_BWD_GROUPS_ALL ? 2 : 0), nullptr,
       (hipStream_t)stream);
   if (e != hipSuccess) return va::fail((int)e, "va_plan_build_device launch: %s", hipGetErrorString(e));
@@ -289,8 +314,7 @@ extern "C" int va_plan_build_device_lengths(const int64_t* lengths_device, int32
     return rc;
   const hipError_t e = va::launch_plan_device(
       nullptr, lengths_device, n_docs, (int)n_tokens, hq, hkv, fwd_items_device, fwd_capacity,
-      bwd_items_device, bwd_capacity, va::bwd_plan_pairs(n_tokens, n_docs, hq, hkv, VA_PLAN_BWD),
-      0, cu_seqlens_out, (hipStream_t)stream);
+      bwd_items_device, bwd_capacity, VA_PLAN_BWD, 0, cu_seqlens_out, (hipStream_t)stream);
   if (e != hipSuccess)
     return va::fail((int)e, "va_plan_build_device_lengths launch: %s", hipGetErrorString(e));
   return VA_OK;

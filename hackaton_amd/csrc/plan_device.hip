@@ -59,14 +59,15 @@ __device__ long long block_scan(long long x, long long* buf, long long cap = 0) 
 
 // At most one of `cu` (int32, n_docs + 1 bounds) and `lengths` (int64, n_docs) is non-null (both
 // null only when n_docs is 0).
-// Work-group 0 builds the forward plan (and writes cu_out when it is non-null), work-group 1 the
-// backward plan; a null item pointer skips that kind.
+// Work-group 0 builds the forward plan, work-group 1 the backward plan; a null item pointer skips
+// that kind. cu_out (when non-null) is written by work-group 0, or by work-group 1 when there is
+// no forward plan.
 __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu,
                                                   const int64_t* __restrict__ lengths, int n_docs,
                                                   int n_tokens, int hq, int hkv,
                                                   int4* __restrict__ fwd_items, long fwd_capacity,
                                                   int4* __restrict__ bwd_items, long bwd_capacity,
-                                                  int bwd_pairs, int bwd_groups,
+                                                  int bwd_kind, int bwd_groups,
                                                   int32_t* __restrict__ cu_out) {
   __shared__ int s_bound[kPlanMaxDocs + 1];  // clamped, non-decreasing document bounds
   __shared__ int s_tbase[kPlanMaxDocs + 1];  // exclusive prefix of the per-document tile counts
@@ -78,7 +79,6 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   const long capacity = kind == VA_PLAN_FWD ? fwd_capacity : bwd_capacity;
   if (items == nullptr) return;  // uniform over the work-group
   const int group = hq / hkv;
-  const bool pairs = kind == VA_PLAN_BWD && bwd_pairs;  // kv items of two heads each
 
   // Document bounds, DPB per thread.
   if (lengths != nullptr) {
@@ -129,7 +129,9 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   if (tid == 0 && n_docs > 0) s_bound[n_docs] = n_tokens;
   for (int b = tid; b < kBuckets; b += PT) s_cnt[b] = 0;
   __syncthreads();
-  if (cu_out != nullptr && kind == VA_PLAN_FWD)
+  // cu_out comes from the forward's work-group, or from the backward's when no forward plan is
+  // built (either item pointer may be null)
+  if (cu_out != nullptr && (fwd_items != nullptr ? kind == VA_PLAN_FWD : kind == VA_PLAN_BWD))
     for (int d = tid; d <= n_docs; d += PT) cu_out[d] = s_bound[d];
 
   // Tile counts and their exclusive prefix sum (DPB documents per thread).
@@ -154,6 +156,8 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   __syncthreads();
   const int n_tiles = s_tbase[n_docs];
   const int n_cand = kind == VA_PLAN_FWD ? n_tiles : 2 * n_tiles;
+  // kv items of two heads each: the host planner's rule over the same tile count
+  const bool pairs = kind == VA_PLAN_BWD && bwd_plan_pairs(n_tiles, hq, hkv, bwd_kind);
 
   // Candidate c -> (document, tile, is_q): kv tiles first, then q tiles (backward).
   auto decode = [&](int c, int& doc, int& t, int& is_q) {
@@ -299,11 +303,11 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
 
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
-                              int32_t* bwd_items, long bwd_capacity, bool bwd_pairs,
+                              int32_t* bwd_items, long bwd_capacity, int bwd_kind,
                               int bwd_groups, int32_t* cu_out, hipStream_t stream) {
   hipLaunchKernelGGL(plan_kernel, dim3(2), dim3(PT), 0, stream, cu, lengths, n_docs, n_tokens, hq,
                      hkv, (int4*)fwd_items, fwd_capacity, (int4*)bwd_items, bwd_capacity,
-                     (int)bwd_pairs, bwd_groups, cu_out);
+                     bwd_kind, bwd_groups, cu_out);
   return hipGetLastError();
 }
 

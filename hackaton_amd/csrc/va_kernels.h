@@ -11,8 +11,9 @@ constexpr int kHeadDim = 128;  // Qwen2.5-1.5B / 7B head size; the kernels are b
 // Tile geometry; the plan builder (plan.cpp) emits work items for exactly these shapes.
 constexpr int kFwdWaves = 4;                 // forward: 32 queries per wave
 constexpr int kFwdBlockM = 32 * kFwdWaves;   // queries per forward work item
-// From this many forward items on (VA_FWD_MANY_ITEMS), the 4-wave forward (two work-groups per
-// CU) runs instead of the 8-wave one: every CU then gets at least two items.
+// From this many 128-query tiles x query heads on (ceil(N / 128) Hq >= VA_FWD_MANY_ITEMS, a lower
+// bound of the forward list's length that host and device plans share), the 4-wave forward (two
+// work-groups per CU) runs instead of the 8-wave one: every CU then gets at least two items.
 constexpr int kFwdLeanMinItems = 512;
 constexpr int kBwdBlockN = 128;  // keys per backward kv work item
 constexpr int kBwdBlockQ = 32;   // queries per kv-item step
@@ -25,7 +26,8 @@ constexpr int kPlanKvItemCost = 39;
 constexpr int kPlanQItemCost = 30;
 constexpr int kPlanCus = 256;  // compute units the plans balance work over (MI355X)
 // VA_PLAN_BWD takes two query heads per item (pair items, Hq > Hkv) once the per-head list
-// would be this long (2 (ceil(N / 128) + n_docs) Hq items: every CU then holds several).
+// would be this long (2 T Hq items, T the 128-row tiles of the documents: every CU then holds
+// several).
 constexpr int kBwdPairMinItems = 1024;
 // Item word: kind << 24 | group << 21 | pair << 20 | (heads - 1) << 12 | head.
 constexpr int kItemPairBit = 1 << 20;
@@ -52,11 +54,13 @@ __host__ __device__ inline int bwd_group_heads(int64_t steps, int group, int64_t
     else if (!subsets) break;
   return 0;
 }
-// Whether a backward plan of `kind` for these host-known sizes has pair items.
-inline bool bwd_plan_pairs(int64_t n_tokens, int32_t n_docs, int32_t hq, int32_t hkv, int kind) {
+// Whether a backward plan of `kind` has pair items; `tiles` = sum over the documents of
+// ceil(length / 128) (empty documents have none), which the host planner and the device planner
+// both count from the same bounds, so that host and device plans of one batch take the same shape.
+__host__ __device__ inline bool bwd_plan_pairs(int64_t tiles, int32_t hq, int32_t hkv, int kind) {
   if (kind == 2 || hkv <= 0 || hq / hkv < 2) return false;  // VA_PLAN_BWD_HEADS, or no group
   if (kind == 3) return true;                                  // VA_PLAN_BWD_PAIRS
-  return 2 * ((n_tokens + 127) / 128 + n_docs) * (int64_t)hq >= kBwdPairMinItems;
+  return 2 * tiles * (int64_t)hq >= kBwdPairMinItems;
 }
 
 struct FwdArgs {
@@ -72,6 +76,7 @@ struct FwdArgs {
   float scale;
   int dtype;
   hipStream_t stream;
+  int kernel;  // 1: the 8-wave forward, 2: the many-item (4-wave) forward
 };
 
 struct BwdArgs {
@@ -95,6 +100,8 @@ struct BwdArgs {
   void* dv;
   uint32_t* flags;  // (n_tokens) 1 where a group item wrote dK/dV itself (the GQA sum skips the
                     // row), 0 where per-head partials hold it; null when Hq == Hkv
+  float* stats;     // (hq, n_tokens) x {lse log2 e, rowsum(dO * O)} written by the row-statistics
+                    // pass before the main kernel, or null: the main kernel forms them itself
   hipStream_t stream;
 };
 
@@ -123,7 +130,8 @@ struct RopeArgs {
 
 hipError_t launch_fwd(const FwdArgs& a);
 hipError_t launch_bwd(const BwdArgs& a);
-hipError_t launch_bwd_stage(const BwdArgs& a, int stage);  // 1 main, 2 finish, 3 finish (no flags)
+// stage 1 main (reads a.stats when non-null), 2 finish, 3 finish (no flags), 4 row statistics
+hipError_t launch_bwd_stage(const BwdArgs& a, int stage);
 hipError_t launch_rope_fwd(const RopeArgs& a);
 hipError_t launch_rope_bwd(const RopeArgs& a);
 hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t* t_idx,
@@ -133,9 +141,11 @@ hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, co
 // Device-built plans (plan_device.hip): from a device cu_seqlens or from device lengths (exactly
 // one non-null); each requested plan (non-null items) is `capacity` items, real ones first, empty
 // ones after; cu_out (nullable) receives the clamped document bounds.
+// bwd_kind: the backward plan kind whose pair rule applies (bwd_plan_pairs over the tiles that the
+// device counts).
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
-                              int32_t* bwd_items, long bwd_capacity, bool bwd_pairs,
+                              int32_t* bwd_items, long bwd_capacity, int bwd_kind,
                               int bwd_groups,
                               int32_t* cu_out, hipStream_t stream);
 

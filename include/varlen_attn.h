@@ -55,7 +55,8 @@ enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1, VA_PLAN_BWD_HEADS = 2, VA_PLAN_BWD_PAIR
        VA_PLAN_BWD_GROUPS = 4, VA_PLAN_BWD_GROUPS_ALL = 5 };
 enum { VA_BWD_PAIR_MIN_ITEMS = 1024 };
 enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
-enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2, VA_BWD_FINISH_HEADS = 3 };
+enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2, VA_BWD_FINISH_HEADS = 3, VA_BWD_STATS = 4,
+       VA_BWD_MAIN_STATS = 5 };
 
 const char* va_last_error(void);
 int32_t va_abi_version(void);
@@ -66,8 +67,9 @@ int32_t va_head_dim(void);
  * backward (one per 128-key tile for dK/dV and one per 128-query tile for dQ, each x query
  * head (VA_PLAN_BWD_HEADS) or x pair of query heads of one GQA group, the last head of an odd
  * group alone (VA_PLAN_BWD_PAIRS); VA_PLAN_BWD takes pairs when Hq > Hkv
- * and the per-head list would hold 2 (ceil(n_tokens / 128) + n_docs) Hq >= VA_BWD_PAIR_MIN_ITEMS
- * items, heads otherwise) over the documents of cu_seqlens, longest first. The items of one tile
+ * and the per-head list would hold 2 T Hq >= VA_BWD_PAIR_MIN_ITEMS items, T = the sum over the
+ * documents of ceil(length / 128), heads otherwise; a device-built plan applies the same rule to
+ * the same count) over the documents of cu_seqlens, longest first. The items of one tile
  * and GQA group sit 8 apart in the list (work-group i runs on XCD i mod 8), so that the heads
  * sharing K/V run on one XCD and share its L2. Fully masked causal tiles and cross-document tiles
  * never appear. VA_PLAN_BWD_GROUPS is VA_PLAN_BWD with GQA group items where they do not lengthen
@@ -77,8 +79,9 @@ int32_t va_head_dim(void);
  * of S = G heads writes the tile's dK/dV itself (Hkv width): no per-head partials, nothing for
  * the GQA sum; one of S < G heads writes the sum of its heads into the first head's partial.
  * Item word: kind << 24 | group << 21 | pair << 20 | (S - 1) << 12 | head.
- * VA_PLAN_BWD_GROUPS_ALL gives every key tile S = G. Group plans need dk/dv in va_bwd (their
- * partials are not per head) and Hq > Hkv. Every plan kind gives the same outputs up to rounding
+ * VA_PLAN_BWD_GROUPS_ALL gives every key tile S = G. Group plans need Hq > Hkv; with dk = dv =
+ * NULL their per-head partials hold each group item's sum in its first head (see va_bwd). Every
+ * plan kind gives the same outputs up to rounding
  * (a pair item sums a head's steps or tiles in one sequence instead of two halves, a group item
  * its heads' in one); each is deterministic.
  * Replaces: solution/attention.py:195-209 (_cu_seqlens, cached per lengths by the caller). */
@@ -86,6 +89,16 @@ int va_plan_size(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t 
                  int64_t* n_items);
 int va_plan_build(const int32_t* cu_seqlens, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind,
                   int32_t* items, int64_t capacity, int64_t* n_items);
+
+/* Whether the backward's row statistics pay for a pass of their own (VA_BWD_STATS, then
+ * VA_BWD_MAIN_STATS instead of VA_BWD_MAIN) over the documents of cu_seqlens: *use = 1 when the
+ * query rows are covered by VA_BWD_STATS_MIN_TILES or more 128-key tiles on average (a row's
+ * tiles are those at or before its own in its document: each one's kv item stages the row).
+ * The pass reads O and dO once (2 Hq D e bytes per row); without it every kv item that covers a
+ * row loads its O beside dO to form rowsum(dO * O). Host only, no GPU call. No counterpart in
+ * the reference (its aten kernel's internal choice). */
+enum { VA_BWD_STATS_MIN_TILES = 3 };
+int va_plan_bwd_row_stats(const int32_t* cu_seqlens, int32_t n_docs, int32_t* use);
 
 /* ---- work plan built on the device --------------------------------------------------------------
  * For callers whose document lengths live on the GPU: the plan is built from a device cu_seqlens
@@ -124,24 +137,34 @@ int va_stream_capture_id(void* stream, uint64_t* capture_id);
 /* ---- attention forward ------------------------------------------------------------------------
  * out = softmax(scale q k^T + causal mask per document) v, lse = log-sum-exp of each row;
  * scale must be finite and > 0 (D^-0.5 in the reference).
- * From VA_FWD_MANY_ITEMS items on (n_items, empty items included) va_fwd runs its many-item
- * kernel (4 waves per item, two work-groups per CU) instead of the 8-wave one; both compute the
- * same function (results agree to rounding, each is deterministic).
+ * From ceil(total_tokens / 128) * Hq >= VA_FWD_MANY_ITEMS on (a lower bound of the list's length
+ * that depends on the sizes only, so host and device plans of one batch pick the same kernel)
+ * va_fwd runs its many-item kernel (4 waves per item, two work-groups per CU) instead of the
+ * 8-wave one; both compute the same function (results agree to rounding, each is deterministic).
+ * va_fwd_kernel is va_fwd with the kernel named: VA_FWD_AUTO (va_fwd's choice), VA_FWD_WIDE (the
+ * 8-wave kernel) or VA_FWD_MANY (the many-item kernel), for callers that time or test one of them.
  * Replaces: solution/attention.py:221-222 (aten::_efficient_attention_forward). */
 enum { VA_FWD_MANY_ITEMS = 512 };
+enum { VA_FWD_AUTO = 0, VA_FWD_WIDE = 1, VA_FWD_MANY = 2 };
 int va_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
            const int32_t* items, int64_t n_items, int64_t total_tokens, int32_t hq, int32_t hkv,
            int32_t head_dim, float scale, int32_t dtype, void* stream);
+int va_fwd_kernel(int32_t kernel, const void* q, const void* k, const void* v, void* out,
+                  float* lse, const int32_t* items, int64_t n_items, int64_t total_tokens,
+                  int32_t hq, int32_t hkv, int32_t head_dim, float scale, int32_t dtype,
+                  void* stream);
 
 /* ---- attention backward -----------------------------------------------------------------------
  * Deterministic and atomic-free. dq (N, Hq, 128) is always written. dk/dv (N, Hkv, 128) are the
  * sums over each GQA group of per-query-head partials (N, Hq, 128, element type) that live in the
  * workspace at the offsets va_bwd_workspace_layout reports; with dk = dv = NULL the partials are
- * the result (a rotary backward can sum them, as the reference sums its expanded copies; the plan
- * must then have no group items). The workspace ends with one uint32 flag per row, past the two
- * partial arrays, that marks the rows whose dK/dV a group item wrote. With Hq == Hkv and dk/dv
- * given, no workspace is used. The caller's O and lse come from va_fwd;
- * rowsum(dO * O) is computed inside.
+ * the result (a rotary backward can sum them, as the reference sums its expanded copies; a group
+ * item then writes its heads' sum into the partial of its first head and zeros into its other
+ * heads', so that the sum over each GQA group's partials is exact for every plan kind). Past the
+ * two partial arrays the workspace holds one uint32 flag
+ * per row, marking the rows whose dK/dV a group item wrote, then the row statistics of
+ * VA_BWD_STATS. With Hq == Hkv and dk/dv given, va_bwd uses no workspace. The caller's O and lse
+ * come from va_fwd; rowsum(dO * O) is computed inside.
  * Replaces: solution/attention.py:230-232 (aten::_efficient_attention_backward) and the GQA
  * reduction of dk/dv at solution/attention.py:113-134. */
 int va_bwd_workspace_layout(int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim,
@@ -166,7 +189,12 @@ int va_bwd_noalloc(const void* dout, const void* q, const void* k, const void* v
 
 /* The same backward in its two stages, for callers that time or overlap them separately:
  * VA_BWD_MAIN (dQ and the per-head dK/dV partials) and VA_BWD_FINISH (the GQA sums into dk/dv;
- * nothing when they are NULL or Hq == Hkv). VA_BWD_FINISH_HEADS is VA_BWD_FINISH for a list
+ * nothing when they are NULL or Hq == Hkv). VA_BWD_STATS writes the row statistics
+ * {lse log2 e, rowsum(dO * O)} (fp32, (Hq, N) pairs) into the workspace's last region, and
+ * VA_BWD_MAIN_STATS is VA_BWD_MAIN reading them instead of loading O (the caller runs VA_BWD_STATS
+ * first, on the same stream and workspace; both need the workspace even when Hq == Hkv): the
+ * results are bitwise those of VA_BWD_MAIN, which forms the same statistics with the same
+ * arithmetic. VA_BWD_FINISH_HEADS is VA_BWD_FINISH for a list
  * without group items (VA_PLAN_BWD, VA_PLAN_BWD_HEADS, VA_PLAN_BWD_PAIRS, or a VA_PLAN_BWD_GROUPS
  * list in which the planner grouped no key tile): every key row then sums its G per-head
  * partials, so the row flags that group items leave are not read (one dependent memory round

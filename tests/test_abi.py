@@ -15,6 +15,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "varlen_attn.h")
 
 
+def doc_tiles(lengths):
+    """128-row tiles of the documents (empty ones have none)."""
+    return sum(-(-int(x) // 128) for x in lengths if int(x) > 0)
+
+
 def declared_symbols():
     text = open(HEADER).read()
     return sorted(set(re.findall(r"\b(va_[a-z0-9_]+)\s*\(", text)))
@@ -120,7 +125,7 @@ def test_backward_plan_covers_every_key_and_query_tile_once(lengths, hq, hkv, ki
     one head each (heads plans) or two heads of one GQA group, the last head of an odd group
     alone (pairs plans)."""
     g = hq // hkv
-    bound = 2 * (-(-sum(lengths) // 128) + len(lengths)) * hq
+    bound = 2 * doc_tiles(lengths) * hq
     pairs = g > 1 and (kind == _lib.VA_PLAN_BWD_PAIRS or
                        (kind == _lib.VA_PLAN_BWD and bound >= _lib.VA_BWD_PAIR_MIN_ITEMS))
     cu, items = plan(lengths, hq, hkv, kind)
@@ -197,7 +202,7 @@ def test_group_plan_covers_every_tile_once(lengths, hq, hkv, kind):
     assert sorted(covered) == expected
     for (a, e, s), ns in subsets.items():
         assert len(ns) == 1, (a, ns)  # one head count per tile
-    bound = 2 * (-(-sum(lengths) // 128) + len(lengths)) * hq
+    bound = 2 * doc_tiles(lengths) * hq
     pairs = bound >= _lib.VA_BWD_PAIR_MIN_ITEMS
     for a, e, s in {(a, e, s) for a, e, s, w in items.tolist() if w >> 24 == 0}:
         steps = (e - a + 31) // 32
@@ -225,13 +230,15 @@ def test_group_plan_covers_every_tile_once(lengths, hq, hkv, kind):
 
 
 @pytest.mark.parametrize("lengths,pairs", [([512] * 4, False), ([64, 37, 50, 12], False),
-                                           ([4096, 4096], True), ([180] * 45, True)])
+                                           ([4096, 4096], True), ([180] * 45, True),
+                                           ([100] * 42, False), ([100] * 43, True),
+                                           ([0] * 50 + [100] * 42, False)])
 def test_backward_plan_takes_pairs_when_the_list_is_long(lengths, pairs):
-    """VA_PLAN_BWD is the heads plan below VA_BWD_PAIR_MIN_ITEMS per-head items (by the
-    host-known bound 2 (ceil(N / 128) + n_docs) Hq) and the pairs plan from there on."""
+    """VA_PLAN_BWD is the heads plan below VA_BWD_PAIR_MIN_ITEMS per-head items (2 T Hq, T the
+    128-row tiles of the documents, a count the device planner makes from the same bounds) and
+    the pairs plan from there on."""
     hq, hkv = 12, 2
-    n = sum(lengths)
-    bound = 2 * (-(-n // 128) + len(lengths)) * hq
+    bound = 2 * doc_tiles(lengths) * hq
     assert (bound >= _lib.VA_BWD_PAIR_MIN_ITEMS) == pairs
     _, auto = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD)
     _, fixed = plan(lengths, hq, hkv, _lib.VA_PLAN_BWD_PAIRS if pairs else _lib.VA_PLAN_BWD_HEADS)
@@ -284,14 +291,15 @@ def test_attention_entry_points_validate_before_launching():
     nbytes = ctypes.c_int64()
     assert lib.va_bwd_workspace_layout(2048, 12, 2, 128, offs, ctypes.byref(nbytes)) == 0
     assert list(offs) == [0, 2048 * 12 * 256]
-    assert nbytes.value == 2 * 2048 * 12 * 256 + 2048 * 4  # partials, then one flag per row
+    # partials, then one flag per row, then the row statistics (two fp32 per query head and row)
+    assert nbytes.value == 2 * 2048 * 12 * 256 + 2048 * 4 + 2048 * 12 * 8
     rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, fake,
                     None, None, fake, nbytes.value - 1, None)
     assert rc == _lib.VA_ECAPACITY
     rc = lib.va_bwd(fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128, 0.1, 0, fake,
                     fake, None, fake, nbytes.value, None)
     assert rc == _lib.VA_EINVAL and b"both" in lib.va_last_error()
-    for stage in (0, 4):  # only VA_BWD_MAIN, VA_BWD_FINISH and VA_BWD_FINISH_HEADS exist
+    for stage in (0, 6):  # stages 1-5 exist
         rc = lib.va_bwd_stage(stage, fake, fake, fake, fake, fake, fake, fake, 4, 2048, 12, 2, 128,
                               0.1, 0, fake, fake, fake, fake, nbytes.value, None)
         assert rc == _lib.VA_EINVAL and b"stage" in lib.va_last_error()
@@ -360,3 +368,55 @@ def test_header_constants_match_python():
     for name, value in consts.items():
         if hasattr(_lib, name):
             assert getattr(_lib, name) == value, name
+
+
+def test_backward_workspace_only_where_partials_exist():
+    """Hq == Hkv with dK/dV returned (the reference's expanded call) needs no workspace: the
+    kernels write dK/dV directly, so the Python layer allocates none (448 MiB of unused partials
+    at N = 32768, H = 28 otherwise)."""
+    from hackaton_amd.attention import bwd_workspace_needed
+
+    assert not bwd_workspace_needed(12, 12)
+    assert not bwd_workspace_needed(28, 28, outputs=True)
+    assert bwd_workspace_needed(12, 12, outputs=False)  # the partials are the result
+    assert bwd_workspace_needed(12, 2)
+    assert bwd_workspace_needed(28, 4, outputs=False)
+
+
+def test_noalloc_refuses_sizes_beyond_its_scratch():
+    """va_bwd_noalloc checks sizes and arguments on the host before any launch or device query;
+    the fake pointers are never dereferenced."""
+    lib = _lib.lib()
+    scale = 128 ** -0.5
+    limit = lib.va_bwd_noalloc_max_bytes() // (2 * 2 * 128)  # tokens x query heads it holds
+    fake = ctypes.c_void_p(0x1000)
+    n = limit // 12 + 1
+    rc = lib.va_bwd_noalloc(fake, fake, fake, fake, fake, fake, fake, 4, n, 12, 2, 128, scale, 0,
+                            fake, fake, fake, None)
+    assert rc == _lib.VA_ECAPACITY
+    assert b"scratch" in lib.va_last_error()
+    rc = lib.va_bwd_noalloc(fake, fake, fake, fake, fake, fake, fake, 4, 100, 12, 2, 128, scale, 0,
+                            fake, None, None, None)
+    assert rc == _lib.VA_EINVAL
+    assert limit >= 8192 * 12  # configurations 2 and 3 fit
+
+
+def test_row_statistics_rule():
+    """va_plan_bwd_row_stats: the mean over query rows of the 128-key tiles at or before the
+    row's own, against VA_BWD_STATS_MIN_TILES = 3. Closed forms: a document of 128 m rows covers
+    its rows (m + 1) / 2 times on average; configurations 1-4 stay below 3, configuration 5's
+    long documents (3.44) pass."""
+    from hackaton_amd import workloads as wl
+    from hackaton_amd.attention import bwd_row_stats
+
+    assert _lib.VA_BWD_STATS_MIN_TILES == 3
+    assert not bwd_row_stats([0, 128 * 4])       # mean 2.5
+    assert bwd_row_stats([0, 128 * 5])           # mean 3.0
+    assert not bwd_row_stats([0, 128 * 5 - 1])   # 127 rows of the last tile short
+    assert not bwd_row_stats([0, 128 * 5, 128 * 5 + 1])  # one row more, covered once
+    assert not bwd_row_stats([0])                # no documents
+    for cfg, expect in ((1, False), (2, False), (3, False), (4, False), (5, True)):
+        lengths = wl.config_lengths(cfg)
+        assert bwd_row_stats(np.concatenate([[0], np.cumsum(lengths)])) is expect, cfg
+    use = ctypes.c_int32(7)
+    assert _lib.lib().va_plan_bwd_row_stats(None, 1, ctypes.byref(use)) == _lib.VA_EINVAL

@@ -90,8 +90,8 @@ def test_varlen_matches_oracle(lengths, hq, hkv, dtype):
 
 
 def padded_fwd_plan(plan, min_items):
-    """The forward items of `plan` followed by empty items up to `min_items`: a list that long
-    runs the many-item (4-wave, two work-groups per CU) forward kernel on the same real items."""
+    """The forward items of `plan` followed by empty items up to `min_items` (which the kernels
+    skip), as a device-built plan pads its list."""
     items = torch.zeros(max(min_items, plan.n_fwd), 4, dtype=torch.int32, device="cuda")
     items[: plan.n_fwd] = plan.fwd_items[: plan.n_fwd]
     return items
@@ -99,9 +99,10 @@ def padded_fwd_plan(plan, min_items):
 
 @pytest.mark.parametrize("lengths,hq,hkv,dtype", CASES + [([300, 45, 1, 128], 12, 2, "peaky")])
 def test_many_item_forward_matches_oracle(lengths, hq, hkv, dtype):
-    """The forward kernel that runs for plans of many items (>= kFwdLeanMinItems = 512; one wave
-    per query strip over all key tiles, no halves to merge), forced on small cases by padding the
-    plan with empty items: O and lse against the oracle, and the backward run from them."""
+    """The forward kernel that runs for many items (ceil(N / 128) Hq >= VA_FWD_MANY_ITEMS = 512;
+    one wave per query strip over all key tiles, no halves to merge), forced on small cases with
+    va_fwd_kernel(VA_FWD_MANY) over the plan padded with empty items: O and lse against the
+    oracle, and the backward run from them."""
     qk = 3.0 if dtype == "peaky" else 1.0
     dtype = torch.bfloat16 if dtype == "peaky" else dtype
     banner("many-item forward", lengths, hq, hkv, dtype, qk)
@@ -113,9 +114,11 @@ def test_many_item_forward_matches_oracle(lengths, hq, hkv, dtype):
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     out = torch.empty_like(qd)
     lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
-    att.check(att.lib().va_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
-                               lse.data_ptr(), items.data_ptr(), items.shape[0], n, hq, hkv, 128,
-                               SCALE, 0 if dtype == torch.float16 else 1, att._stream()), "va_fwd")
+    att.check(att.lib().va_fwd_kernel(att._lib.VA_FWD_MANY, qd.data_ptr(), kd.data_ptr(),
+                                      vd.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                      items.data_ptr(), items.shape[0], n, hq, hkv, 128, SCALE,
+                                      0 if dtype == torch.float16 else 1, att._stream()),
+              "va_fwd_kernel")
     dq, dk, dv = att.attention_backward(do.to(dev), qd, kd, vd, out, lse, plan, SCALE)
     torch.cuda.synchronize()
     ref = oracle(q, k, v, do, lengths)
@@ -446,12 +449,37 @@ def rope_tables(seq, dim=128, seed=0):
     return emb.cos(), emb.sin()
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_packed_attention_matches_oracle(dtype):
+PACKED_CASES = [
+    # per-head backward list, partials summed by the inverse rotation
+    ("small", [70, 33, 51, 1, 200], 12, 2, torch.float16),
+    ("small", [70, 33, 51, 1, 200], 12, 2, torch.bfloat16),
+    # configuration 3's documents: the partials route over the pair list
+    ("config3", wl.config_lengths(3), 12, 2, torch.float16),
+    # configuration 4's documents: group items write dK/dV at Hkv width, no GQA sum
+    ("config4", wl.config_lengths(4), 12, 2, torch.bfloat16),
+    # the first 8 documents of configuration 5 (7B heads): the row statistics pass
+    ("config5[:8]", wl.config_lengths(5)[:8], 28, 4, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("name,lengths,heads,kv_heads,dtype", PACKED_CASES,
+                         ids=[f"{c[0]}-{c[4]}" for c in PACKED_CASES])
+def test_packed_attention_matches_oracle(name, lengths, heads, kv_heads, dtype):
     """Rotation + attention of the packed rows (PackedAttention) against the oracle: fp32
-    rotation rounded once to the compute type, fp64 attention, fp32 inverse rotation."""
-    lengths, heads, kv_heads = [70, 33, 51, 1, 200], 12, 2
-    banner("packed_attention", lengths, dtype)
+    rotation rounded once to the compute type, fp64 attention, fp32 inverse rotation. Each case
+    checks first that the installed path takes the backward route it is there for."""
+    banner("packed_attention", name, len(lengths), sum(lengths), heads, kv_heads, dtype)
+    plan = att._plan(att._cu_seqlens(lengths, torch.device("cuda")), heads, kv_heads)
+    kv_words = plan.partial_bwd()[0].cpu().numpy()[:, 3]
+    kv_words = kv_words[(kv_words >> 24) == 0]
+    if name == "small":
+        assert att.packed_bwd_sums_heads(plan) and not ((kv_words >> 20) & 1).any()
+    elif name == "config3":
+        assert att.packed_bwd_sums_heads(plan) and ((kv_words >> 20) & 1).all()
+    elif name == "config4":
+        assert not att.packed_bwd_sums_heads(plan) and not plan.bwd_stats
+    else:
+        assert att.packed_bwd_sums_heads(plan) and plan.bwd_stats
     seq = max(lengths)
     rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)])
     b_idx, t_idx = (rows // seq).to(torch.int32), (rows % seq).to(torch.int32)
@@ -547,7 +575,8 @@ def test_device_plan_matches_host_plan(lengths):
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     assert dplan.cu.cpu().numpy().tolist() == cu.tolist()
     groups = att._lib.VA_PLAN_BWD_GROUPS
-    pairs = 2 * (-(-n // 128) + len(lengths)) * hq >= att._lib.VA_BWD_PAIR_MIN_ITEMS
+    tiles = sum(-(-x // 128) for x in lengths if x > 0)
+    pairs = 2 * tiles * hq >= att._lib.VA_BWD_PAIR_MIN_ITEMS
     part_items, part_n = dplan.partial_bwd()
     for kind, items, count in ((0, dplan.fwd_items, dplan.n_fwd), (1, part_items, part_n),
                                (groups, dplan.bwd_items, dplan.n_bwd)):
@@ -620,11 +649,21 @@ def test_device_lengths_plan_is_rebuilt_inside_a_captured_graph():
     assert not torch.equal(captured, eager_first)
 
 
-def test_device_lengths_run_without_host_reads_and_match_host_lengths():
-    """varlen_attention and packed_attention with the lengths as a device tensor (device
-    cu_seqlens and plan, no host read) give bitwise the host-lengths results."""
-    lengths, hq, hkv = [334, 200, 0, 100, 7], 12, 2
-    banner("device lengths", lengths)
+@pytest.mark.parametrize("lengths,hq,hkv", [
+    ([334, 200, 0, 100, 7], 12, 2),
+    # many short documents: the device list's capacity (648) and the host list (360 items) lie on
+    # either side of VA_FWD_MANY_ITEMS; both paths still run the same forward kernel
+    ([100] * 30, 12, 2),
+    # zero lengths beside 43 documents: the host drops them, the device counts them, and both
+    # take pair items by the tiles of the non-empty documents
+    ([0] * 10 + [100] * 43, 12, 2),
+    ([0, 300, 0, 45, 1], 28, 4),
+])
+def test_device_lengths_run_without_host_reads_and_match_host_lengths(lengths, hq, hkv):
+    """varlen_attention with the lengths as a device tensor (device cu_seqlens and plan, no host
+    read) gives bitwise the host-lengths results: both paths choose the forward kernel from the
+    sizes and the backward's pair shape from the tiles of the non-empty documents."""
+    banner("device lengths", len(lengths), sum(lengths), hq, hkv)
     q, k, v, do = wl.make_inputs([x for x in lengths if x], hq, hkv, torch.float16, seed=5)
     host = run_varlen(q, k, v, do, lengths)
     dev_lengths = torch.tensor(lengths, device="cuda")
@@ -785,9 +824,9 @@ def test_kernels_skip_items_of_a_plan_for_other_sizes():
     items = padded_fwd_plan(plan_big, 512)
     ob2, out2 = canaried((n, hq_small, 128), torch.float16)
     lb2, lse2 = canaried((hq_small, n), torch.float32)
-    att.check(lib.va_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out2.data_ptr(),
-                         lse2.data_ptr(), items.data_ptr(), items.shape[0], n, hq_small, hkv, 128,
-                         SCALE, 0, att._stream()), "va_fwd")
+    att.check(lib.va_fwd_kernel(att._lib.VA_FWD_MANY, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                out2.data_ptr(), lse2.data_ptr(), items.data_ptr(), items.shape[0],
+                                n, hq_small, hkv, 128, SCALE, 0, att._stream()), "va_fwd_kernel")
     torch.cuda.synchronize()
     for buf in (ob2, lb2):
         assert torch.isnan(buf[:pad].float()).all() and torch.isnan(buf[-pad:].float()).all()
@@ -832,6 +871,142 @@ def test_gqa_sum_without_flags_matches_flagged_sum(cfg):
         att.check(lib.va_bwd_stage(stage, *argv), "va_bwd_stage")
         res.append((dk, dv))
     torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert not torch.isnan(a.float()).any()
+        assert torch.equal(a, b)
+
+
+STATS_CASES = [
+    ([512, 300, 77, 1], 12, 2, torch.float16, att._lib.VA_PLAN_BWD),         # per-head items
+    (wl.config_lengths(3), 12, 2, torch.float16, att._lib.VA_PLAN_BWD),      # pair items
+    (wl.config_lengths(3), 12, 2, torch.float16, att._lib.VA_PLAN_BWD_GROUPS),
+    ([300, 45, 1, 128], 28, 4, torch.bfloat16, att._lib.VA_PLAN_BWD_GROUPS_ALL),
+    ([64, 37, 50, 12], 12, 12, torch.float16, att._lib.VA_PLAN_BWD),        # Hq == Hkv
+    ([5, 33], 4, 2, torch.bfloat16, att._lib.VA_PLAN_BWD),
+]
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,dtype,kind", STATS_CASES)
+def test_row_statistics_pass_gives_bitwise_the_in_kernel_statistics(lengths, hq, hkv, dtype,
+                                                                      kind):
+    """VA_BWD_STATS + VA_BWD_MAIN_STATS (lse log2 e and rowsum(dO * O) formed once per row by a
+    pass of their own) against VA_BWD_MAIN (formed by every item that stages the row): same
+    arithmetic, so dQ, dK/dV and the per-head partials agree bit for bit, for every item shape."""
+    banner("row statistics pass", len(lengths), sum(lengths), hq, hkv, dtype, kind)
+    dev = torch.device("cuda")
+    lib = att.lib()
+    n = sum(lengths)
+    cu = orc.cu_seqlens_from_lengths(lengths)
+    items_np = att.build_plan_host(cu, hq, hkv, kind)
+    items = torch.from_numpy(items_np).to(dev)
+    fwd = torch.from_numpy(att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_FWD)).to(dev)
+    q, k, v, do = (t.to(dev) for t in wl.make_inputs(lengths, hq, hkv, dtype, seed=11))
+    code = att._lib.VA_F16 if dtype == torch.float16 else att._lib.VA_BF16
+    out = torch.empty_like(q)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+    att.check(lib.va_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                         fwd.data_ptr(), fwd.shape[0], n, hq, hkv, 128, SCALE, code,
+                         att._stream()), "va_fwd")
+    grouped = kind in (att._lib.VA_PLAN_BWD_GROUPS, att._lib.VA_PLAN_BWD_GROUPS_ALL)
+    res = []
+    for stages in ([att._lib.VA_BWD_MAIN], [att._lib.VA_BWD_STATS, att._lib.VA_BWD_MAIN_STATS]):
+        ws = torch.full((att.bwd_workspace(n, hq, hkv, dev)[0].numel(),), 255, dtype=torch.uint8,
+                        device=dev)
+        offs = att.bwd_workspace(n, hq, hkv, dev)[1]
+        dq = torch.full_like(q, float("nan"))
+        dk, dv = torch.full_like(k, float("nan")), torch.full_like(v, float("nan"))
+        outs = [(dk, dv)] if (grouped or hq == hkv) else [(dk, dv), (None, None)]
+        for dk_o, dv_o in outs:
+            argv = (do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                    lse.data_ptr(), items.data_ptr(), items.shape[0], n, hq, hkv, 128, SCALE,
+                    code, dq.data_ptr(), _ptr_or_none(dk_o), _ptr_or_none(dv_o), ws.data_ptr(),
+                    ws.numel(), att._stream())
+            for st in stages + ([att._lib.VA_BWD_FINISH] if dk_o is not None else []):
+                att.check(lib.va_bwd_stage(st, *argv), "va_bwd_stage")
+            torch.cuda.synchronize()
+            part = n * hq * 128 * 2
+            parts = [ws[o: o + part].clone() for o in offs] if dk_o is None else []
+            res.append([dq.clone(), dk.clone(), dv.clone(), *parts])
+    half = len(res) // 2
+    for a, b in zip(res[:half], res[half:]):
+        for x, y in zip(a, b):
+            if x.is_floating_point():
+                assert not torch.isnan(x.float()).any()
+            assert torch.equal(x, y)
+
+
+def _ptr_or_none(t):
+    return t.data_ptr() if t is not None else None
+
+
+def test_device_plan_writes_cu_seqlens_without_a_forward_plan():
+    """va_plan_build_device_lengths with only the backward plan requested still writes
+    cu_seqlens_out (the backward's work-group writes it when there is no forward plan)."""
+    lengths, hq, hkv = [334, 0, 200, 100, 7], 12, 2
+    banner("device plan cu_seqlens, backward only", lengths)
+    dev = torch.device("cuda")
+    n = sum(lengths)
+    cap = np.zeros(1, dtype=np.int64)
+    att.check(att.lib().va_plan_capacity(n, len(lengths), hq, att._lib.VA_PLAN_BWD,
+                                         cap.ctypes.data_as(att._lib._pi64)), "va_plan_capacity")
+    items = torch.empty(int(cap[0]), 4, dtype=torch.int32, device=dev)
+    cu = torch.full((len(lengths) + 1,), -7, dtype=torch.int32, device=dev)
+    lens = torch.tensor(lengths, dtype=torch.int64, device=dev)
+    att.check(att.lib().va_plan_build_device_lengths(lens.data_ptr(), len(lengths), n, hq, hkv,
+                                                     None, 0, items.data_ptr(), int(cap[0]),
+                                                     cu.data_ptr(), att._stream()),
+              "va_plan_build_device_lengths")
+    torch.cuda.synchronize()
+    assert cu.cpu().tolist() == np.concatenate([[0], np.cumsum(lengths)]).tolist()
+    host = att.build_plan_host(np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32), hq,
+                               hkv, att._lib.VA_PLAN_BWD)
+    got = [tuple(x) for x in items.cpu().numpy().tolist() if any(x)]
+    assert sorted(got) == sorted(map(tuple, host.tolist()))
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,kind", [
+    (wl.config_lengths(3), 12, 2, att._lib.VA_PLAN_BWD_GROUPS),      # S = 6, 3 and 2 tiles
+    ([300, 45, 1, 128], 28, 4, att._lib.VA_PLAN_BWD_GROUPS_ALL),
+    ([512, 300, 77, 1], 12, 2, att._lib.VA_PLAN_BWD_GROUPS_ALL),
+])
+def test_group_items_without_outputs_leave_exact_partials(lengths, hq, hkv, kind):
+    """A group-item list run with dk = dv = NULL (the partials are the result): each group item
+    writes its heads' sum into its first head's partial and zeros into the others', so the sum of
+    all G partials of a row (VA_BWD_FINISH_HEADS, no row flags) is bitwise the dK/dV that the same
+    list writes with outputs (group items at Hkv width, the flagged GQA sum for S < G)."""
+    banner("group items without outputs", len(lengths), sum(lengths), hq, hkv, kind)
+    dev = torch.device("cuda")
+    lib = att.lib()
+    n = sum(lengths)
+    cu = orc.cu_seqlens_from_lengths(lengths)
+    items = torch.from_numpy(att.build_plan_host(cu, hq, hkv, kind)).to(dev)
+    fwd = torch.from_numpy(att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_FWD)).to(dev)
+    q, k, v, do = (t.to(dev) for t in wl.make_inputs(lengths, hq, hkv, torch.float16, seed=13))
+    out = torch.empty_like(q)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+    att.check(lib.va_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                         fwd.data_ptr(), fwd.shape[0], n, hq, hkv, 128, SCALE, 0, att._stream()),
+              "va_fwd")
+    res = []
+    for outputs in (True, False):
+        ws = torch.full((att.bwd_workspace(n, hq, hkv, dev)[0].numel(),), 0x7f, dtype=torch.uint8,
+                        device=dev)  # stale partials: 0x7f7f is a NaN in fp16
+        dq = torch.empty_like(q)
+        dk, dv = torch.full_like(k, float("nan")), torch.full_like(v, float("nan"))
+
+        def argv(with_out):
+            return (do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                    lse.data_ptr(), items.data_ptr(), items.shape[0], n, hq, hkv, 128, SCALE, 0,
+                    dq.data_ptr(), dk.data_ptr() if with_out else None,
+                    dv.data_ptr() if with_out else None, ws.data_ptr(), ws.numel(),
+                    att._stream())
+        if outputs:
+            att.check(lib.va_bwd(*argv(True)), "va_bwd")
+        else:
+            att.check(lib.va_bwd_stage(att._lib.VA_BWD_MAIN, *argv(False)), "va_bwd_stage")
+            att.check(lib.va_bwd_stage(att._lib.VA_BWD_FINISH_HEADS, *argv(True)), "va_bwd_stage")
+        torch.cuda.synchronize()
+        res.append((dq.clone(), dk.clone(), dv.clone()))
     for a, b in zip(*res):
         assert not torch.isnan(a.float()).any()
         assert torch.equal(a, b)
