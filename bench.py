@@ -19,7 +19,7 @@ Also reported on the same JSON line:
   (profiles/hbm_traffic_<workload>.md);
 * by_config: the same fwd+bwd call timed at BASELINE configurations 3-5;
 * installed_path: PackedAttention (rotation, attention forward, attention backward, inverse
-  rotation with the GQA sum) as the decoder layer calls it, at the headline configuration (host
+  rotation) as the decoder layer calls it, at the headline configuration (host
   and device lengths) and at configurations 3-5 (host lengths), beside the bare kernels' time;
 * cpu_baseline: the reference's own CPU-runnable math (torch CPU scaled_dot_product_attention in
   fp32, forward + autograd backward, GQA through enable_gqa), in the two constructions the
@@ -418,8 +418,9 @@ def time_config(cfg, reps):
 
 
 def time_installed_path(cfg, reps, with_device_lengths=False):
-    """PackedAttention as the patched decoder layer calls it (rotation, attention forward and
-    backward, inverse rotation with the GQA sum) at one configuration, captured in a graph with
+    """PackedAttention as the patched decoder layer calls it (rotation, attention forward, attention
+    backward and the inverse rotation, in its epilogues or as a pass of its own) at one
+    configuration, captured in a graph with
     its autograd backward; with host lengths (cached host plan) and, if asked, device lengths
     (cu_seqlens and plan built on the device in every call). Each document is one padded batch
     row of the decoder's input (b_idx = document, t_idx = position), as the reference's packed
@@ -457,9 +458,11 @@ def time_installed_path(cfg, reps, with_device_lengths=False):
     flops = wl.attention_flops(lengths, hq) * n_sets
     plan = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
     res = {"workload": c["name"], "buffer_sets": n_sets,
-           "backward": ("per-head partials summed by the inverse rotation"
-                        if att.packed_bwd_sums_heads(plan) else
-                        "dK/dV at Hkv width from group items, then the rotation"),
+           "backward": (("inverse rotation in the backward kernels' epilogues; "
+                         + ("GQA sum of rotated partials" if plan.bwd_finish else
+                            "group items write dK/dV at Hkv width, no GQA sum"))
+                        if att.rotary_epilogues(n, hq) else
+                        "per-head partials summed by the inverse rotation pass"),
            "row_statistics_pass": bool(plan.bwd_stats)}
     variants = [("host_lengths", lengths)]
     if with_device_lengths:

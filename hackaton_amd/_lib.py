@@ -27,6 +27,13 @@ _f32 = ctypes.c_float
 _pi32 = ctypes.POINTER(ctypes.c_int32)
 _pi64 = ctypes.POINTER(ctypes.c_int64)
 
+class RopeTables(ctypes.Structure):
+    """va_rope_tables: the rotary tables of va_bwd_rotary_stage's epilogues."""
+    _fields_ = [("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+                ("cos_batch_stride", ctypes.c_int64), ("cos_seq_stride", ctypes.c_int64),
+                ("b_idx", ctypes.c_void_p), ("t_idx", ctypes.c_void_p)]
+
+
 # name -> (restype, argtypes); the same list the header declares.
 SIGNATURES = {
     "va_last_error": (ctypes.c_char_p, []),
@@ -52,6 +59,9 @@ SIGNATURES = {
                                       _f32, _i32, _p, _p, _p, _p]),
     "va_bwd_stage": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                     _f32, _i32, _p, _p, _p, _p, _i64, _p]),
+    "va_bwd_rotary_stage": (ctypes.c_int, [_i32, ctypes.POINTER(RopeTables), _p, _p, _p, _p, _p,
+                                           _p, _p, _i64, _i64, _i32, _i32, _i32, _f32, _i32, _p,
+                                           _p, _p, _p, _i64, _p]),
     "va_rope_fwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i32,
                                    _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "va_rope_bwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i32,

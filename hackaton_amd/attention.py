@@ -15,9 +15,10 @@ Differences that keep the drop-in contract:
 * `varlen_attention` accepts key/value with Hkv heads (GQA-native: the kernels read each key/value
   head once for its G query heads) as well as the reference's expanded Hq-head form.
 * `packed_attention` rotates q and k without expanding K/V to the query heads and runs the
-  attention on Hkv key/value heads; the backward kernels write dQ and per-query-head dK/dV, and
-  the inverse rotation sums the G heads of each group in fp32 (the reference sums its expanded
-  fp16 copies the same way, solution/attention.py:113-134). The backward is deterministic.
+  attention on Hkv key/value heads; its backward sums dK/dV over each GQA group in fp32 (the
+  reference sums its expanded fp16 copies, solution/attention.py:113-134) and rotates dQ and dK
+  back, in the backward kernels' epilogues for long lists, else in a pass of its own. The
+  backward is deterministic.
 * fp16 and bf16 inputs both run on the MFMA kernels (the reference computes in fp16 only).
 
 Every op requires the HIP library and CUDA (HIP) tensors; there is no other implementation.
@@ -301,10 +302,12 @@ def bwd_stages(plan, outputs=True, workspace=True):
     return stages
 
 
-def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=True):
+def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=True, rope=None):
     """dq, dk, dv of packed causal attention (dk/dv summed over each GQA group), deterministic.
     With outputs=False returns dq and the per-query-head dK/dV partials (N, Hq, D) in the element
-    type (plus the workspace that holds them), for a caller that sums them itself."""
+    type (plus the workspace that holds them), for a caller that sums them itself. With `rope`
+    (rotary_tables(...)) dq and dk come out rotated back to the projections' frame by the
+    kernels' epilogues (va_bwd_rotary_stage)."""
     n, hq, d = query.shape
     hkv = key.shape[1]
     dtype = _attn_dtype(query)
@@ -327,7 +330,11 @@ def attention_backward(grad, query, key, value, out, lse, plan, scale, outputs=T
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws.numel() if ws is not None else 0,
             _stream())
     for stage in bwd_stages(plan, outputs, ws is not None):
-        check(lib().va_bwd_stage(stage, *argv), "va_bwd_stage")
+        if rope is None:
+            check(lib().va_bwd_stage(stage, *argv), "va_bwd_stage")
+        else:
+            check(lib().va_bwd_rotary_stage(stage, ctypes.byref(rope[0]), *argv),
+                  "va_bwd_rotary_stage")
     if outputs:
         return dq, dk, dv
     part = n * hq * d * 2
@@ -397,6 +404,19 @@ def _tables(cos, sin):
     if cos.shape != sin.shape or cos.dim() != 3 or cos.shape[-1] != HEAD_DIM:
         raise ValueError(f"cos/sin must be (1 or B, T, {HEAD_DIM}), got {tuple(cos.shape)}")
     return cos, sin
+
+
+def rotary_tables(cos, sin, b_idx, t_idx):
+    """The va_rope_tables of a packed call (fp32 cos/sin (1 or B, T, D), int32 token rows and
+    positions) and the tensors it points to (kept alive beside it)."""
+    _require_device(cos, sin, b_idx, t_idx)
+    cos, sin = _tables(cos, sin)
+    b_idx = b_idx.to(torch.int32).contiguous()
+    t_idx = t_idx.to(torch.int32).contiguous()
+    scb, sct = _rope_strides(cos)
+    tab = _lib.RopeTables(cos.data_ptr(), sin.data_ptr(), scb, sct, b_idx.data_ptr(),
+                          t_idx.data_ptr())
+    return tab, (cos, sin, b_idx, t_idx)
 
 
 def rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads, out_dtype, layout=0,
@@ -513,22 +533,26 @@ def set_save_policy(policy):
     SAVE_POLICY = policy
 
 
-def packed_bwd_sums_heads(plan):
-    """Whether PackedAttention's backward leaves per-query-head dK/dV partials for the inverse
-    rotation to sum (one pass over them instead of a GQA sum and a rotation): where the plan's
-    backward would launch its GQA sum. Where it would not (every key tile in group items that
-    cover the whole GQA group, or Hq == Hkv), the main kernel writes dK/dV at Hkv width and the
-    rotation reads those."""
-    return bool(getattr(plan, "bwd_finish", True))
+def rotary_epilogues(n_tokens, heads):
+    """Whether PackedAttention's backward rotates dQ and dK back in the attention kernels'
+    epilogues (va_bwd_rotary_stage) rather than leaving per-head partials to the standalone
+    inverse rotation. The epilogues read the fp32 tables (1 KB per row) once per query head and
+    row, where the standalone pass reads them once per token, but save that pass's round trip of
+    dQ and the partials: they pay where the lists hold many items (ceil(N / 128) Hq >=
+    VA_FWD_MANY_ITEMS; measured at configurations 3-5: 125 -> 114, 231 -> 223, 1419 -> 1394 us per
+    layer call), and lose at a few long items (configuration 2: 50.0 -> 51.9 us), whose epilogues
+    then set the time. A rule of the sizes only, so host and device lengths take the same route."""
+    return _lib.fwd_many_items(n_tokens, heads)
 
 
 class PackedAttention(torch.autograd.Function):
     """Autograd node of the decoder layer's call: rotary embedding, then causal attention of every
     document of the packed rows; returns (N, heads * D) in the compute type.
 
-    The backward runs the attention backward kernels and the inverse rotation: the rotation sums
-    per-query-head dK/dV partials over each GQA group in fp32, or, where the plan's group items
-    write dK/dV at Hkv width (packed_bwd_sums_heads), rotates those. What is kept for it follows
+    The backward runs the attention backward kernels and the inverse rotation: in the kernels'
+    epilogues (dQ and dK rotated back in fp32 before their one rounding) where the lists are long,
+    else as a pass of its own that sums per-query-head dK/dV partials over each GQA group in fp32
+    while it rotates (rotary_epilogues). What is kept for it follows
     SAVE_POLICY: the rotated operands, O and lse ("outputs"), or only the three projections,
     recomputing the rotation and the forward like solution/attention.py:250-279 ("inputs", and
     always when `offload` moves them to pinned host memory). Returns the three projection
@@ -565,18 +589,23 @@ class PackedAttention(torch.autograd.Function):
             q, k, v = OFFLOADER.load(ctx.item) if hasattr(ctx, "item") else ctx.saved_tensors
             out, lse, (qr, kr, vr), plan = _attend(q, k, v, cos, sin, b_idx, t_idx, seq, heads,
                                                    kv_heads, lengths, scale)
-        if packed_bwd_sums_heads(plan):
-            # dq and the per-query-head dK/dV partials; the inverse rotation sums the partials
-            # over each GQA group (as solution/attention.py:113-134 sums its expanded copies)
-            dq_r, dk_r, dv_r, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
-                                                       outputs=False)
-        else:
-            # the plan's group items (or Hq == Hkv) write dK/dV at Hkv width themselves
-            dq_r, dk_r, dv_r = attention_backward(dout, qr, kr, vr, out, lse, plan, scale)
         q_dtype, k_dtype, v_dtype = ctx.dtypes
-        dq, dk, dv = rope_backward(dq_r, dk_r, dv_r, cos, sin, b_idx, t_idx, heads, kv_heads,
-                                   q_dtype, expand=packed_bwd_sums_heads(plan))
-        grads = (dq, dk.to(k_dtype), dv.to(v_dtype))
+        n = qr.shape[0]
+        if rotary_epilogues(n, heads):
+            # the inverse rotation in the attention backward's epilogues: dq and dk come out as
+            # the projections' gradients, dK/dV summed over each GQA group by group items or the
+            # GQA sum of rotated partials (solution/attention.py:113-134 sums expanded copies)
+            dq, dk, dv = attention_backward(dout, qr, kr, vr, out, lse, plan, scale,
+                                            rope=rotary_tables(cos, sin, b_idx, t_idx))
+            dq, dk, dv = dq.reshape(n, -1), dk.reshape(n, -1), dv.reshape(n, -1)
+        else:
+            # dq and the per-query-head dK/dV partials; the inverse rotation sums the partials
+            # over each GQA group in fp32 while it rotates (as attention.py:113-134 sums copies)
+            dq_r, dk_part, dv_part, _ws = attention_backward(dout, qr, kr, vr, out, lse, plan,
+                                                             scale, outputs=False)
+            dq, dk, dv = rope_backward(dq_r, dk_part, dv_part, cos, sin, b_idx, t_idx, heads,
+                                       kv_heads, q_dtype, expand=True)
+        grads = (dq.to(q_dtype), dk.to(k_dtype), dv.to(v_dtype))
         return (*grads, None, None, None, None, None, None, None, None, None, None)
 
 

@@ -121,9 +121,24 @@ int bwd_checked(int32_t stage, const void* dout, const void* q, const void* k, c
                 const void* out, const float* lse, const int32_t* items, int64_t n_items,
                 int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim, float scale,
                 int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+                int64_t workspace_bytes, void* stream, const va_rope_tables* rope) {
   int rc = check_attn_shape(total_tokens, hq, hkv, head_dim);
   if (rc) return rc;
+  va::RopeTab tab{nullptr, nullptr, nullptr, nullptr, 0, 0};
+  if (rope != nullptr) {
+    if (rope->cos == nullptr || rope->sin == nullptr || rope->b_idx == nullptr ||
+        rope->t_idx == nullptr)
+      return va::fail(VA_EINVAL, "va_bwd_rotary_stage: NULL rotary table or index");
+    if (!aligned16(rope->cos) || !aligned16(rope->sin))
+      return va::fail(VA_EINVAL, "va_bwd_rotary_stage: cos/sin not 16-byte aligned");
+    if (rope->cos_batch_stride < 0 || rope->cos_seq_stride < 0 ||
+        rope->cos_batch_stride % 4 != 0 || rope->cos_seq_stride % 4 != 0 ||
+        rope->cos_batch_stride > INT32_MAX || rope->cos_seq_stride > INT32_MAX)
+      return va::fail(VA_EINVAL,
+                      "va_bwd_rotary_stage: cos/sin strides must be non-negative multiples of 4");
+    tab = va::RopeTab{rope->cos, rope->sin, rope->b_idx, rope->t_idx,
+                      (int)rope->cos_batch_stride, (int)rope->cos_seq_stride};
+  }
   if ((rc = check_dtype16(dtype))) return rc;
   if (n_items < 0 || n_items > INT32_MAX) return va::fail(VA_EINVAL, "n_items out of range");
   if (!std::isfinite(scale) || scale <= 0.f)
@@ -156,7 +171,7 @@ int bwd_checked(int32_t stage, const void* dout, const void* q, const void* k, c
   float* stats = with_stats ? reinterpret_cast<float*>(ws + 2 * offs[1] + round256(total_tokens * 4))
                             : nullptr;
   va::BwdArgs a{dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv, scale, dtype,
-                dq, dk_part, dv_part, dk, dv, flags, stats, (hipStream_t)stream};
+                dq, dk_part, dv_part, dk, dv, flags, stats, (hipStream_t)stream, tab};
   const int kstage = stage == VA_BWD_MAIN_STATS ? 1 : stage == VA_BWD_STATS ? 4 : stage;
   hipError_t e = stage < 0 ? va::launch_bwd(a) : va::launch_bwd_stage(a, kstage);
   return e == hipSuccess ? VA_OK : hip_fail(e, "va_bwd launch");
@@ -170,7 +185,8 @@ extern "C" int va_bwd(const void* dout, const void* q, const void* k, const void
                       int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
                       int64_t workspace_bytes, void* stream) {
   return va::bwd_checked(-1, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
-                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
+                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream,
+                         nullptr);
 }
 
 extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k,
@@ -183,7 +199,24 @@ extern "C" int va_bwd_stage(int32_t stage, const void* dout, const void* q, cons
       stage != VA_BWD_STATS && stage != VA_BWD_MAIN_STATS)
     return va::fail(VA_EINVAL, "va_bwd_stage: stage %d", stage);
   return va::bwd_checked(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
-                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream);
+                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream,
+                         nullptr);
+}
+
+extern "C" int va_bwd_rotary_stage(int32_t stage, const va_rope_tables* rope, const void* dout,
+                                   const void* q, const void* k, const void* v, const void* out,
+                                   const float* lse, const int32_t* items, int64_t n_items,
+                                   int64_t total_tokens, int32_t hq, int32_t hkv,
+                                   int32_t head_dim, float scale, int32_t dtype, void* dq,
+                                   void* dk, void* dv, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  if (stage != VA_BWD_MAIN && stage != VA_BWD_FINISH && stage != VA_BWD_FINISH_HEADS &&
+      stage != VA_BWD_STATS && stage != VA_BWD_MAIN_STATS)
+    return va::fail(VA_EINVAL, "va_bwd_rotary_stage: stage %d", stage);
+  if (rope == nullptr) return va::fail(VA_EINVAL, "va_bwd_rotary_stage: rope is NULL");
+  return va::bwd_checked(stage, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
+                         head_dim, scale, dtype, dq, dk, dv, workspace, workspace_bytes, stream,
+                         rope);
 }
 
 namespace {

@@ -70,7 +70,7 @@ __device__ __host__ constexpr int block_c(int b, int /*i*/) { return b; }
 // SHAPE (item word bits 20-21): 0 per head, 1 pair, 2 group; a template constant, so that each
 // shape's step loop carries no unit / head arithmetic of the others (per-head items: no division
 // by the step count, no pair selects).
-template <class E, int SHAPE, bool PREP>
+template <class E, int SHAPE, bool PREP, bool ROPE>
 __device__ __forceinline__ void bwd_kv_item(
     lds_u16* smem, float (&stat)[2][2][2][bwd::BQ], const int4 it,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -78,7 +78,8 @@ __device__ __forceinline__ void bwd_kv_item(
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     uint16_t* __restrict__ dk_part, uint16_t* __restrict__ dv_part, uint16_t* __restrict__ dk_out,
     uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags, int n_tokens, int hq, int hkv,
-    float scale, float scale_log2, const f32x2* __restrict__ stats) {
+    float scale, float scale_log2, const f32x2* __restrict__ stats, const RopeTab& rope,
+    int* trow_lds) {
   using namespace bwd;
   const int k0 = it.x, doc_end = it.y, h = it.w & kHeadMask;
   constexpr bool pair = SHAPE == 1;
@@ -93,6 +94,10 @@ __device__ __forceinline__ void bwd_kv_item(
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
   const int kw0 = k0 + 32 * strip;
   const int my_key = kw0 + l32;
+  // Rotary table row of this lane's key, looked up with the prologue's loads and parked in LDS
+  // (a register held across the step loop would spill there), so that the epilogue's table loads
+  // wait for no other memory access.
+  if constexpr (ROPE) trow_lds[tid] = (int)rope_row(rope, min(my_key, doc_end - 1));
 
   // K and V tiles, row-major, rows clamped to the document: loaded here, stored to LDS once the
   // first step pair's loads are in flight too (one memory round trip for the whole prologue).
@@ -382,6 +387,63 @@ __device__ __forceinline__ void bwd_kv_item(
     store_rows32<16>(reinterpret_cast<lds_u16*>(&xs[slot(half, 0, 0) - lane]), w, lane,
                     [&](int r) { return part + ((long)(kw0 + r) * rs + hd) * D; }, doc_end - kw0);
   };
+  // With rotary tables the halves split the columns instead of the tensors: half H finishes dK
+  // and dV for accumulators db = 2 H, 2 H + 1 with both column halves c, i.e. the (d, d + 64)
+  // pairs that the inverse rotation of dK mixes (registers [8 c, 8 c + 8) hold d = 16 db + 64 c +
+  // 8 hi + 0..7), so each half rotates half of dK with the tables of 16 pairs, loaded before the
+  // exchange. Same exchange volume; each tensor goes out as two 64-byte runs per row.
+  auto xslot = [&](int dst, int t, int j, int j4) {
+    return (((dst * NS + strip) * 2 + t) * 8 + 4 * j + j4) * 64 + lane;
+  };
+  auto finish_rot = [&](auto half_c, uint16_t* kout, uint16_t* vout, int rs, int hd) {
+    constexpr int H = decltype(half_c)::value;
+    const int trow = trow_lds[tid];
+    Tab8 tab[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) tab[j] = load_tab8(rope, trow, 16 * (2 * H + j) + 8 * hi);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+          const f32x16& a = t ? dvacc[2 * (1 - H) + j] : dkacc[2 * (1 - H) + j];
+          xs[xslot(H ^ 1, t, j, j4)] = f32x4{a[4 * j4], a[4 * j4 + 1], a[4 * j4 + 2], a[4 * j4 + 3]};
+        }
+    __syncthreads();
+    u32x4 wk[4], wv[4];  // w[j + 2 c]: registers [8 c, 8 c + 8) of accumulator 2 H + j
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float xk[16], xv[16];
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const f32x4 yk = xs[xslot(H, 0, j, j4)], yv = xs[xslot(H, 1, j, j4)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xk[4 * j4 + e] = (dkacc[2 * H + j][4 * j4 + e] + yk[e]) * scale;
+          xv[4 * j4 + e] = dvacc[2 * H + j][4 * j4 + e] + yv[e];
+        }
+      }
+      rope_unrotate8(tab[j], xk);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        wk[j + 2 * c] = pack8<E>(xk[8 * c], xk[8 * c + 1], xk[8 * c + 2], xk[8 * c + 3],
+                                 xk[8 * c + 4], xk[8 * c + 5], xk[8 * c + 6], xk[8 * c + 7]);
+        wv[j + 2 * c] = pack8<E>(xv[8 * c], xv[8 * c + 1], xv[8 * c + 2], xv[8 * c + 3],
+                                 xv[8 * c + 4], xv[8 * c + 5], xv[8 * c + 6], xv[8 * c + 7]);
+      }
+    }
+    // through two row tiles in this wave's own (just read) exchange slots; tile column
+    // t = 16 j + 32 c + 8 hi + e holds d = t + 32 H + 32 c
+    lds_u16* tk = reinterpret_cast<lds_u16*>(&xs[xslot(H, 0, 0, 0) - lane]);
+    lds_u16* tv = reinterpret_cast<lds_u16*>(&xs[xslot(H, 1, 0, 0) - lane]);
+    static_assert(32 * (8 * 8 + 8) * 2 <= 8 * 64 * 16, "a row tile fits in one tensor's slots");
+    auto cols = [](int col) { return col + 32 * H + (col >= 32 ? 32 : 0); };
+    store_rows32<8>(tk, wk, lane, [&](int r) { return kout + ((long)(kw0 + r) * rs + hd) * D; },
+                    doc_end - kw0, cols);
+    store_rows32<8>(tv, wv, lane, [&](int r) { return vout + ((long)(kw0 + r) * rs + hd) * D; },
+                    doc_end - kw0, cols);
+  };
   // The GQA sum reads how many heads each partial of a row sums (S; G: a group item wrote the
   // row's dK/dV itself): every key row belongs to one tile, whose items of the GQA group's first
   // head write its flag. Without outputs every head's partial holds a share (zeros beside a
@@ -416,20 +478,48 @@ __device__ __forceinline__ void bwd_kv_item(
                         doc_end - kw0);
       }
     };
+    if constexpr (ROPE) {  // dK back to the projection's frame, in place (next tables ahead)
+      const int trow = trow_lds[tid];
+      Tab8 t0 = load_tab8(rope, trow, 8 * hi), t1;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        if (db + 1 < 4) t1 = load_tab8(rope, trow, 16 * (db + 1) + 8 * hi);
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = dkacc[db][i];
+        rope_unrotate8(t0, x);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dkacc[db][i] = x[i];
+        t0 = t1;
+      }
+    }
     store(dkacc, scale, dk_part);
     store(dvacc, 1.f, dv_part);
     return;
   }
   if (S == G && dk_out != nullptr) {
-    if (half) finish(dvacc, dkacc, 1.f, dv_out, hkv, kvh);
-    else finish(dkacc, dvacc, scale, dk_out, hkv, kvh);
+    if constexpr (ROPE) {
+      if (half) finish_rot(std::integral_constant<int, 1>{}, dk_out, dv_out, hkv, kvh);
+      else finish_rot(std::integral_constant<int, 0>{}, dk_out, dv_out, hkv, kvh);
+    } else if (half) {
+      finish(dvacc, dkacc, 1.f, dv_out, hkv, kvh);
+    } else {
+      finish(dkacc, dvacc, scale, dk_out, hkv, kvh);
+    }
   } else {
-    if (half) finish(dvacc, dkacc, 1.f, dv_part, hq, h);
-    else finish(dkacc, dvacc, scale, dk_part, hq, h);
+    if constexpr (ROPE) {
+      if (half) finish_rot(std::integral_constant<int, 1>{}, dk_part, dv_part, hq, h);
+      else finish_rot(std::integral_constant<int, 0>{}, dk_part, dv_part, hq, h);
+    } else if (half) {
+      finish(dvacc, dkacc, 1.f, dv_part, hq, h);
+    } else {
+      finish(dkacc, dvacc, scale, dk_part, hq, h);
+    }
     if constexpr (grouped) {
       // No outputs: the caller sums all G per-head partials of each row, so the item's other
       // heads' partials hold zeros (its sum went into head h's), and that sum is exact.
       if (dk_out == nullptr) {
+        // half j clears tensor j (dK / dV) of the other heads
         uint16_t* part = half ? dv_part : dk_part;
         for (int x = 1; x < S; ++x)
           for (int i = lane; i < 32 * (D / 8); i += 64) {
@@ -447,13 +537,14 @@ __device__ __forceinline__ void bwd_kv_item(
 // one GQA group: then half j takes head h + j over both tiles of every pair, so the halves share
 // the K/V tiles, never exchange dQ, and each writes all 128 columns of its head.
 // --------------------------------------------------------------------------------------------
-template <class E, bool PAIR, bool PREP>
+template <class E, bool PAIR, bool PREP, bool ROPE>
 __device__ __forceinline__ void bwd_q_item(
     lds_u16* smem, const int4 it, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, uint16_t* __restrict__ dq, int n_tokens, int hq, int hkv,
-    float scale, float scale_log2, float* stat_f, const f32x2* __restrict__ stats) {
+    float scale, float scale_log2, float* stat_f, const f32x2* __restrict__ stats,
+    const RopeTab& rope, int* trow_lds) {
   using namespace bwd;
   const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kHeadMask;
   constexpr bool pair = PAIR;
@@ -464,6 +555,8 @@ __device__ __forceinline__ void bwd_q_item(
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
   const int wq0 = q0 + 32 * strip;
   const int my_q = wq0 + l32;
+  // Rotary table row of this lane's query, looked up with the prologue's loads, parked in LDS.
+  if constexpr (ROPE) trow_lds[tid] = (int)rope_row(rope, min(my_q, doc_end - 1));
 
   const int kv_end = min(q0 + QB, doc_end);
   const int n_tiles = (kv_end - doc_start + BT - 1) / BT;
@@ -639,6 +732,21 @@ __device__ __forceinline__ void bwd_q_item(
   }
 
   if (pair) {
+    if constexpr (ROPE) {  // dQ back to the projection's frame, in place (next tables ahead)
+      const int trow = trow_lds[tid];
+      Tab8 t0 = load_tab8(rope, trow, 8 * hi), t1;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        if (db + 1 < 4) t1 = load_tab8(rope, trow, 16 * (db + 1) + 8 * hi);
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = dqacc[db][i];
+        rope_unrotate8(t0, x);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dqacc[db][i] = x[i];
+        t0 = t1;
+      }
+    }
     // Each half holds its head's whole dQ^T: 64 columns at a time through this wave's own row
     // tile (the LDS is free after the loop's last barrier), scaled.
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -700,13 +808,65 @@ __device__ __forceinline__ void bwd_q_item(
                     [&](int r) { return dq + (long)(wq0 + r) * qrow + h * D + 64 * H; },
                     doc_end - wq0);
   };
-  if (half) finish(std::integral_constant<int, 1>{});
-  else finish(std::integral_constant<int, 0>{});
+  // With rotary tables half H finishes instead accumulators db = 2 H, 2 H + 1 with both column
+  // halves c, i.e. the (d, d + 64) pairs that the inverse rotation mixes: d in [32 H, 32 H + 32)
+  // and [64 + 32 H, 96 + 32 H), two 64-byte runs per row. Same exchange volume.
+  auto finish_rot = [&](auto half_c) {
+    constexpr int H = decltype(half_c)::value;
+    const int trow = trow_lds[tid];
+    Tab8 tab[2];  // issued before the exchange, which hides their latency
+#pragma unroll
+    for (int j = 0; j < 2; ++j) tab[j] = load_tab8(rope, trow, 16 * (2 * H + j) + 8 * hi);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j2 = 0; j2 < 2; ++j2) {
+          const f32x16& a = dqacc[2 * (1 - H) + j];
+          const int r = 8 * c + 4 * j2;
+          xq[qslot(H ^ 1, 2 * j + c, j2)] = f32x4{a[r], a[r + 1], a[r + 2], a[r + 3]};
+        }
+    __syncthreads();
+    u32x4 w[4];  // w[j + 2 c]: registers [8 c, 8 c + 8) of accumulator 2 H + j
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const f32x16& a = dqacc[2 * H + j];
+      float x[16];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j2 = 0; j2 < 2; ++j2) {
+          const f32x4 y = xq[qslot(H, 2 * j + c, j2)];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            x[8 * c + 4 * j2 + e] = (a[8 * c + 4 * j2 + e] + y[e]) * scale;
+        }
+      rope_unrotate8(tab[j], x);
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        w[j + 2 * c] = pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3],
+                                x[8 * c + 4], x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]);
+    }
+    // tile column t = 16 j + 32 c + 8 hi + e holds d = t + 32 H + 32 c
+    store_rows32<8>(reinterpret_cast<lds_u16*>(&xq[qslot(H, 0, 0) - lane]), w, lane,
+                    [&](int r) { return dq + (long)(wq0 + r) * qrow + h * D; }, doc_end - wq0,
+                    [](int col) { return col + 32 * H + (col >= 32 ? 32 : 0); });
+  };
+  if constexpr (ROPE) {
+    if (half) finish_rot(std::integral_constant<int, 1>{});
+    else finish_rot(std::integral_constant<int, 0>{});
+  } else if (half) {
+    finish(std::integral_constant<int, 1>{});
+  } else {
+    finish(std::integral_constant<int, 0>{});
+  }
 }
 
 // PREP: lse log2 e and delta come from the row-statistics pass (`stats`); otherwise the items
-// load O beside dO and form delta themselves.
-template <class E, bool PREP>
+// load O beside dO and form delta themselves. ROPE: dQ and dK are rotated back with `rope`'s
+// tables before they are stored.
+template <class E, bool PREP, bool ROPE>
 // Arguments in the order the work-group needs them: the first 14 dwords are preloaded into
 // SGPRs at launch (-amdgpu-kernarg-preload-count), so the work item's load starts at once.
 __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
@@ -716,10 +876,11 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     const float* __restrict__ lse, uint16_t* __restrict__ dq, uint16_t* __restrict__ dk_part,
     uint16_t* __restrict__ dv_part, int n_tokens, float scale, float scale_log2,
     uint16_t* __restrict__ dk_out, uint16_t* __restrict__ dv_out, uint32_t* __restrict__ flags,
-    const f32x2* __restrict__ stats) {
+    const f32x2* __restrict__ stats, RopeTab rope) {
   __shared__ __attribute__((aligned(16))) uint16_t smem_raw[bwd::HALFS];
   __shared__ __attribute__((aligned(16))) float stat[2][2][2][bwd::BQ];  // [stage][lse|del][half]
   __shared__ __attribute__((aligned(16))) float qstat[4 * bwd::QB];  // q items: [head][lse|del]
+  __shared__ int trow_lds[ROPE ? bwd::NT : 1];  // rotary table row of each thread's key / query
   lds_u16* smem = (lds_u16*)smem_raw;
   const int4 it = items[blockIdx.x];
   // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
@@ -736,20 +897,23 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
     return;
   if (kind == bwd::kKindKV) {
     if (shape == 0)
-      bwd_kv_item<E, 0, PREP>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
-                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats);
+      bwd_kv_item<E, 0, PREP, ROPE>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats,
+                              rope, trow_lds);
     else if (shape == 1)
-      bwd_kv_item<E, 1, PREP>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
-                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats);
+      bwd_kv_item<E, 1, PREP, ROPE>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats,
+                              rope, trow_lds);
     else
-      bwd_kv_item<E, 2, PREP>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
-                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats);
+      bwd_kv_item<E, 2, PREP, ROPE>(smem, stat, it, q, k, v, out, dout, lse, dk_part, dv_part, dk_out,
+                              dv_out, flags, n_tokens, hq, hkv, scale, scale_log2, stats,
+                              rope, trow_lds);
   } else if (shape == 0) {
-    bwd_q_item<E, false, PREP>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
-                               scale_log2, qstat, stats);
+    bwd_q_item<E, false, PREP, ROPE>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
+                               scale_log2, qstat, stats, rope, trow_lds);
   } else {
-    bwd_q_item<E, true, PREP>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
-                              scale_log2, qstat, stats);
+    bwd_q_item<E, true, PREP, ROPE>(smem, it, q, k, v, out, dout, lse, dq, n_tokens, hq, hkv, scale,
+                              scale_log2, qstat, stats, rope, trow_lds);
   }
 }
 
@@ -757,23 +921,23 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
 // Row statistics of the backward, once per (query head, row): {lse log2 e, delta = rowsum(dO * O)}
 // in fp32, with the arithmetic of the items' own staging (16 threads per row, v_dot2 over each
 // thread's 8 elements, then the 16-lane DPP sum), so that the main kernel's results do not depend
-// on where delta was formed. Work-group: 64 rows of one head, 4 rows per thread (8 loads in
-// flight each). Rows past n_tokens are not touched.
+// on where delta was formed. Rows are taken in memory order (token-major, all heads of a token
+// are adjacent), 64 per work-group, 4 per thread (8 loads in flight each).
 // --------------------------------------------------------------------------------------------
 constexpr int kStatThreads = 256, kStatRows = 64;
 template <class E>
 __global__ __launch_bounds__(kStatThreads) void bwd_stats_kernel(
     const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout,
     const float* __restrict__ lse, f32x2* __restrict__ stats, int n_tokens, int hq) {
-  const int h = blockIdx.y, tid = threadIdx.x;
-  const int r0 = blockIdx.x * kStatRows + (tid >> 4), col = 8 * (tid & 15);
-  const long qrow = (long)hq * kHeadDim;
+  const int tid = threadIdx.x;
+  const long rows = (long)n_tokens * hq;
+  const long r0 = (long)blockIdx.x * kStatRows + (tid >> 4);
+  const int col = 8 * (tid & 15);
   constexpr int R = kStatRows / (kStatThreads / 16);
   u32x4 o[R], g[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int r = min(r0 + 16 * i, n_tokens - 1);
-    const long at = r * qrow + (long)h * kHeadDim + col;
+    const long at = min(r0 + 16 * i, rows - 1) * kHeadDim + col;
     o[i] = gload16(out + at);
     g[i] = gload16(dout + at);
   }
@@ -783,9 +947,10 @@ __global__ __launch_bounds__(kStatThreads) void bwd_stats_kernel(
 #pragma unroll
     for (int w = 0; w < 4; ++w) d = E::dot2(o[i][w], g[i][w], d);
     d = sum_rows16(d);
-    const int r = r0 + 16 * i;
-    if ((tid & 15) == 0 && r < n_tokens) {
-      const long at = (long)h * n_tokens + r;
+    const long r = r0 + 16 * i;
+    if ((tid & 15) == 0 && r < rows) {
+      const int token = (int)(r / hq), h = (int)(r - (long)token * hq);
+      const long at = (long)h * n_tokens + token;
       stats[at] = f32x2{lse[at] * kLog2e, d};
     }
   }
@@ -844,23 +1009,24 @@ __global__ __launch_bounds__(kSumThreads) void bwd_gqa_sum_kernel(const uint16_t
 template <class E>
 static hipError_t launch_bwd_stats_t(const BwdArgs& a) {
   if (a.n_tokens == 0 || a.stats == nullptr) return hipSuccess;
-  const dim3 grid((unsigned)((a.n_tokens + kStatRows - 1) / kStatRows), (unsigned)a.hq);
+  const dim3 grid((unsigned)((a.n_tokens * a.hq + kStatRows - 1) / kStatRows));
   hipLaunchKernelGGL(bwd_stats_kernel<E>, grid, dim3(kStatThreads), 0, a.stream,
                      (const uint16_t*)a.out, (const uint16_t*)a.dout, a.lse, (f32x2*)a.stats,
                      (int)a.n_tokens, a.hq);
   return hipGetLastError();
 }
 
-// PREP: the row statistics are in a.stats already (written by launch_bwd_stats_t).
-template <class E, bool PREP>
+// PREP: the row statistics are in a.stats already (written by launch_bwd_stats_t); ROPE: a.rope
+// holds the rotary tables.
+template <class E, bool PREP, bool ROPE>
 static hipError_t launch_bwd_main_t(const BwdArgs& a) {
   if (a.n_items == 0) return hipSuccess;
-  hipLaunchKernelGGL((bwd_kernel<E, PREP>), dim3((unsigned)a.n_items), dim3(bwd::NT), 0,
+  hipLaunchKernelGGL((bwd_kernel<E, PREP, ROPE>), dim3((unsigned)a.n_items), dim3(bwd::NT), 0,
                      a.stream, (const int4*)a.items, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.out, (const uint16_t*)a.dout, a.hq,
                      a.hkv, a.lse, (uint16_t*)a.dq, (uint16_t*)a.dk_part, (uint16_t*)a.dv_part,
                      (int)a.n_tokens, a.scale, a.scale * kLog2e, (uint16_t*)a.dk,
-                     (uint16_t*)a.dv, a.flags, (const f32x2*)a.stats);
+                     (uint16_t*)a.dv, a.flags, (const f32x2*)a.stats, a.rope);
   return hipGetLastError();
 }
 
@@ -882,9 +1048,15 @@ hipError_t launch_bwd_stage(const BwdArgs& a, int stage) {
   const bool bf = a.dtype != 0;
   if (stage == 4) return bf ? launch_bwd_stats_t<BF16>(a) : launch_bwd_stats_t<F16>(a);
   if (stage == 1) {
-    if (a.stats != nullptr)
-      return bf ? launch_bwd_main_t<BF16, true>(a) : launch_bwd_main_t<F16, true>(a);
-    return bf ? launch_bwd_main_t<BF16, false>(a) : launch_bwd_main_t<F16, false>(a);
+    const bool prep = a.stats != nullptr, rope = a.rope.cos != nullptr;
+    if (bf) {
+      if (rope) return prep ? launch_bwd_main_t<BF16, true, true>(a)
+                            : launch_bwd_main_t<BF16, false, true>(a);
+      return prep ? launch_bwd_main_t<BF16, true, false>(a) : launch_bwd_main_t<BF16, false, false>(a);
+    }
+    if (rope) return prep ? launch_bwd_main_t<F16, true, true>(a)
+                          : launch_bwd_main_t<F16, false, true>(a);
+    return prep ? launch_bwd_main_t<F16, true, false>(a) : launch_bwd_main_t<F16, false, false>(a);
   }
   const bool heads_only = stage == 3;
   return bf ? launch_bwd_finish_t<BF16>(a, heads_only) : launch_bwd_finish_t<F16>(a, heads_only);

@@ -74,7 +74,7 @@ extern "C" int va_bwd_noalloc(const void* dout, const void* q, const void* k, co
   if (rc) return rc;
   if (hq == hkv || total_tokens == 0)  // no partials: dK/dV are written directly
     return va::bwd_checked(-1, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
-                           head_dim, scale, dtype, dq, dk, dv, nullptr, 0, stream);
+                           head_dim, scale, dtype, dq, dk, dv, nullptr, 0, stream, nullptr);
   if (need > kNoAllocScratchBytes)
     return va::fail(VA_ECAPACITY,
                     "va_bwd_noalloc: total_tokens=%lld x Hq=%d needs %lld bytes of dK/dV "
@@ -89,5 +89,6 @@ extern "C" int va_bwd_noalloc(const void* dout, const void* q, const void* k, co
   void* ws = nullptr;
   if ((rc = scratch_of(device, &ws))) return rc;
   return va::bwd_checked(-1, dout, q, k, v, out, lse, items, n_items, total_tokens, hq, hkv,
-                         head_dim, scale, dtype, dq, dk, dv, ws, kNoAllocScratchBytes, stream);
+                         head_dim, scale, dtype, dq, dk, dv, ws, kNoAllocScratchBytes, stream,
+                         nullptr);
 }

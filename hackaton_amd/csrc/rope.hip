@@ -188,8 +188,10 @@ __device__ inline void fwd_store(const RopeArgs& a, long pid, int b, int t, int 
   cvt8<IN>(in.h2, x2);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    y1[e] = sl.is_v ? x1[e] : x1[e] * tb.cs1[e] - x2[e] * tb.sn1[e];
-    y2[e] = sl.is_v ? x2[e] : x2[e] * tb.cs2[e] + x1[e] * tb.sn2[e];
+    float r1, r2;
+    rope_rotate(x1[e], x2[e], tb.cs1[e], tb.cs2[e], tb.sn1[e], tb.sn2[e], r1, r2);
+    y1[e] = sl.is_v ? x1[e] : r1;
+    y2[e] = sl.is_v ? x2[e] : r2;
   }
   for (int r = 0; r < copies; ++r) {
     const int oh = (!sl.is_q && a.expand) ? sl.head * rep + r : sl.head;
@@ -270,8 +272,10 @@ __device__ inline void bwd_store(const RopeArgs& a, long pid, int b, int t, int 
   float o1[8], o2[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    o1[e] = sl.is_v ? d1[e] : d1[e] * tb.cs1[e] + d2[e] * tb.sn2[e];
-    o2[e] = sl.is_v ? d2[e] : d2[e] * tb.cs2[e] - d1[e] * tb.sn1[e];
+    float r1, r2;
+    rope_unrotate(d1[e], d2[e], tb.cs1[e], tb.cs2[e], tb.sn1[e], tb.sn2[e], r1, r2);
+    o1[e] = sl.is_v ? d1[e] : r1;
+    o2[e] = sl.is_v ? d2[e] : r2;
   }
   const gvoid y = pick3(sl.is_q, sl.is_v, a.y0, a.y1, a.y2);
   const long orow = (pid * (sl.is_q ? uniform(a.heads) : uniform(a.kv_heads)) + sl.head) * D;

@@ -242,10 +242,14 @@ __device__ inline void gstore16(uint16_t* p, u32x4 v) {
 // used by this wave only): lane (l32, hi) holds in w[i] the columns 8 (2 i + hi) + 0..7 of row
 // l32. Each global store instruction then writes 64 / C whole rows of 16 C bytes (C lanes x 16
 // bytes per row) instead of 32-byte pieces of 32 rows. Rows >= n_rows are skipped; row_ptr(r)
-// is the global address of column 0 of row r.
-template <int C, class RowPtr>
+// is the global address of column 0 of row r, and tile column c (a multiple of 8) goes to
+// global column col_map(c).
+struct SameColumn {
+  __device__ int operator()(int col) const { return col; }
+};
+template <int C, class RowPtr, class ColMap = SameColumn>
 __device__ inline void store_rows32(lds_u16* tile, const u32x4 (&w)[C / 2], int lane,
-                                    RowPtr row_ptr, int n_rows) {
+                                    RowPtr row_ptr, int n_rows, ColMap col_map = ColMap{}) {
   static_assert(C == 8 || C == 16, "64 or 128 columns");
   constexpr int LT = 8 * C + 8;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -256,7 +260,7 @@ __device__ inline void store_rows32(lds_u16* tile, const u32x4 (&w)[C / 2], int 
   for (int i = 0; i < C / 2; ++i) {
     const int r = (64 / C) * i + r0;
     const u32x4 v = ld128(tile + r * LT + col);
-    if (r < n_rows) gstore16(row_ptr(r) + col, v);
+    if (r < n_rows) gstore16(row_ptr(r) + col_map(col), v);
   }
 }
 
@@ -278,6 +282,52 @@ __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 // inserted before their first use in the loop also waits, on every iteration, for the loads that
 // the loop itself has issued since (the wait counters complete in order).
 __device__ inline void settle(const u32x4& v) { asm volatile("" ::"v"(v)); }
+
+// ---------------------------------------------------------------------------------------------
+// Rotary embedding of a (x[d], x[d + 64]) pair in fp32 with tables c1 = cos[d], c2 = cos[d + 64],
+// s1 = sin[d], s2 = sin[d + 64] (solution/attention.py:57-63), and its inverse, the gradient of the
+// unrotated pair (attention.py:125-134). Written with explicit fused multiply-adds, so that every
+// kernel that rotates (the standalone rotary kernels and the attention kernels' epilogues) rounds
+// the same way.
+// ---------------------------------------------------------------------------------------------
+__device__ inline void rope_rotate(float x1, float x2, float c1, float c2, float s1, float s2,
+                                   float& y1, float& y2) {
+  y1 = __builtin_fmaf(x1, c1, -(x2 * s1));
+  y2 = __builtin_fmaf(x2, c2, x1 * s2);
+}
+__device__ inline void rope_unrotate(float d1, float d2, float c1, float c2, float s1, float s2,
+                                     float& o1, float& o2) {
+  o1 = __builtin_fmaf(d1, c1, d2 * s2);
+  o2 = __builtin_fmaf(d2, c2, -(d1 * s1));
+}
+
+// The table row (element offset) of a packed token.
+__device__ inline long rope_row(const RopeTab& r, int token) {
+  return (long)r.b_idx[token] * r.scb + (long)r.t_idx[token] * r.sct;
+}
+// The tables of 8 (d, d + 64) pairs, d = d0 .. d0 + 7 (d0 < 64, a multiple of 8), of one row:
+// loaded apart from their use, so that an epilogue can issue them before it waits for anything.
+struct Tab8 {
+  f32x4 c1[2], c2[2], s1[2], s2[2];
+};
+__device__ inline Tab8 load_tab8(const RopeTab& r, long row, int d0) {
+  const f32x4* c1 = reinterpret_cast<const f32x4*>(r.cos + row + d0);
+  const f32x4* c2 = reinterpret_cast<const f32x4*>(r.cos + row + 64 + d0);
+  const f32x4* s1 = reinterpret_cast<const f32x4*>(r.sin + row + d0);
+  const f32x4* s2 = reinterpret_cast<const f32x4*>(r.sin + row + 64 + d0);
+  return Tab8{{c1[0], c1[1]}, {c2[0], c2[1]}, {s1[0], s1[1]}, {s2[0], s2[1]}};
+}
+// Inverse rotation, in place, of the 8 (x[e], x[8 + e]) pairs of one lane: x[e] holds element
+// d0 + e of a row, x[8 + e] element d0 + 64 + e, `t` their tables.
+__device__ inline void rope_unrotate8(const Tab8& t, float* x) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    rope_unrotate(x[e], x[8 + e], t.c1[e >> 2][e & 3], t.c2[e >> 2][e & 3], t.s1[e >> 2][e & 3],
+                  t.s2[e >> 2][e & 3], x[e], x[8 + e]);
+}
+__device__ inline void rope_unrotate8(const RopeTab& r, long row, int d0, float* x) {
+  rope_unrotate8(load_tab8(r, row, d0), x);
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;

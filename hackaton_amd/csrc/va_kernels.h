@@ -79,6 +79,16 @@ struct FwdArgs {
   int kernel;  // 1: the 8-wave forward, 2: the many-item (4-wave) forward
 };
 
+// Rotary tables of the attention kernels' epilogues: fp32 cos / sin rows (1 or B, T, 128) at
+// b * scb + t * sct (elements, multiples of 4), b = b_idx[token], t = t_idx[token].
+struct RopeTab {
+  const float* cos;
+  const float* sin;
+  const int32_t* b_idx;
+  const int32_t* t_idx;
+  int scb, sct;
+};
+
 struct BwdArgs {
   const void* dout;
   const void* q;
@@ -103,6 +113,8 @@ struct BwdArgs {
   float* stats;     // (hq, n_tokens) x {lse log2 e, rowsum(dO * O)} written by the row-statistics
                     // pass before the main kernel, or null: the main kernel forms them itself
   hipStream_t stream;
+  RopeTab rope;  // cos null: none; else dQ and dK are written rotated back to the projections'
+                 // frame
 };
 
 struct RopeArgs {

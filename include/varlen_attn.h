@@ -207,6 +207,32 @@ int va_bwd_stage(int32_t stage, const void* dout, const void* q, const void* k, 
                  int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* The backward with the inverse rotary embedding in its epilogues, for a caller whose q and k are
+ * rotated projections (the decoder layer's packed call): dq and dk come out as the gradients of
+ * the projections before the rotation, dv as before. The main stages (VA_BWD_MAIN,
+ * VA_BWD_MAIN_STATS) rotate each finished dQ row and each dK row or per-head dK partial back
+ * with the tables, in fp32 before the one rounding (the rotation is linear, so the GQA sum of
+ * rotated partials is the rotated sum); the other stages are va_bwd_stage's. The tables are those
+ * of va_rope_bwd (fp32, row b * cos_batch_stride + t * cos_seq_stride for the token's b_idx and
+ * t_idx, strides non-negative multiples of 4, cos/sin 16-byte aligned); the caller guarantees
+ * that every token's row lies inside them. Arguments otherwise as va_bwd_stage.
+ * Replaces: solution/attention.py:230-232 followed by the inverse rotation of qkv_kernel mode 1
+ * (attention.py:86-134, launched at 185-187) for dq and dk. */
+typedef struct va_rope_tables {
+  const float* cos;
+  const float* sin;
+  int64_t cos_batch_stride;
+  int64_t cos_seq_stride;
+  const int32_t* b_idx;
+  const int32_t* t_idx;
+} va_rope_tables;
+int va_bwd_rotary_stage(int32_t stage, const va_rope_tables* rope, const void* dout,
+                        const void* q, const void* k, const void* v, const void* out,
+                        const float* lse, const int32_t* items, int64_t n_items,
+                        int64_t total_tokens, int32_t hq, int32_t hkv, int32_t head_dim,
+                        float scale, int32_t dtype, void* dq, void* dk, void* dv, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
 /* ---- rotary embedding -------------------------------------------------------------------------
  * Forward: q (N, heads*D), k, v (N, kv_heads*D) in in_dtype (VA_F16/VA_BF16/VA_F32); cos, sin
  * fp32 tables indexed at b*cos_batch_stride + t*cos_seq_stride (b, t from b_idx/t_idx, int32).

@@ -9,6 +9,8 @@ Tolerances (element type of the inputs; the oracle runs in fp64 on the same 16-b
         computes in fp16 only).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -450,36 +452,45 @@ def rope_tables(seq, dim=128, seed=0):
 
 
 PACKED_CASES = [
-    # per-head backward list, partials summed by the inverse rotation
+    # per-head backward list, rotated partials summed by the GQA sum without row flags
     ("small", [70, 33, 51, 1, 200], 12, 2, torch.float16),
     ("small", [70, 33, 51, 1, 200], 12, 2, torch.bfloat16),
-    # configuration 3's documents: the partials route over the pair list
+    # configuration 3's documents: group items of 6, 3 and 2 heads beside pair items, flagged sum
     ("config3", wl.config_lengths(3), 12, 2, torch.float16),
-    # configuration 4's documents: group items write dK/dV at Hkv width, no GQA sum
+    # configuration 4's documents: group items write rotated dK and dV at Hkv width, no GQA sum
     ("config4", wl.config_lengths(4), 12, 2, torch.bfloat16),
     # the first 8 documents of configuration 5 (7B heads): the row statistics pass
     ("config5[:8]", wl.config_lengths(5)[:8], 28, 4, torch.bfloat16),
+    # expanded K/V (Hq == Hkv): dK/dV written directly, no workspace
+    ("mha", [70, 33, 51, 1, 200], 4, 4, torch.float16),
 ]
 
 
 @pytest.mark.parametrize("name,lengths,heads,kv_heads,dtype", PACKED_CASES,
                          ids=[f"{c[0]}-{c[4]}" for c in PACKED_CASES])
 def test_packed_attention_matches_oracle(name, lengths, heads, kv_heads, dtype):
-    """Rotation + attention of the packed rows (PackedAttention) against the oracle: fp32
-    rotation rounded once to the compute type, fp64 attention, fp32 inverse rotation. Each case
-    checks first that the installed path takes the backward route it is there for."""
+    """Rotation + attention of the packed rows (PackedAttention, the inverse rotation in the
+    backward kernels' epilogues) against the oracle: fp32 rotation rounded once to the compute
+    type, fp64 attention, fp32 inverse rotation. Each case checks first that the plan has the
+    backward shape it is there for."""
     banner("packed_attention", name, len(lengths), sum(lengths), heads, kv_heads, dtype)
     plan = att._plan(att._cu_seqlens(lengths, torch.device("cuda")), heads, kv_heads)
-    kv_words = plan.partial_bwd()[0].cpu().numpy()[:, 3]
-    kv_words = kv_words[(kv_words >> 24) == 0]
-    if name == "small":
-        assert att.packed_bwd_sums_heads(plan) and not ((kv_words >> 20) & 1).any()
-    elif name == "config3":
-        assert att.packed_bwd_sums_heads(plan) and ((kv_words >> 20) & 1).all()
-    elif name == "config4":
-        assert not att.packed_bwd_sums_heads(plan) and not plan.bwd_stats
-    else:
-        assert att.packed_bwd_sums_heads(plan) and plan.bwd_stats
+    words = plan.bwd_items.cpu().numpy()[:, 3]
+    kv_shapes = set(((words[(words >> 24) == 0] >> 20) & 3).tolist())  # 0 head, 1 pair, 2 group
+    q_shapes = set(((words[(words >> 24) == 1] >> 20) & 3).tolist())
+    n = sum(lengths)
+    # short lists: the partials route and the inverse rotation pass; long: the rotary epilogues
+    assert att.rotary_epilogues(n, heads) == (name not in ("small", "mha"))
+    if name == "small":  # per-head q items, per-head and group kv items
+        assert q_shapes == {0} and kv_shapes == {0, 2} and plan.bwd_finish
+    elif name == "config3":  # pair q items, group kv items of 6, 3 and 2 heads, flagged sum
+        assert q_shapes == {1} and kv_shapes == {2} and plan.bwd_finish
+    elif name == "config4":  # group kv items of the whole group everywhere: no GQA sum
+        assert kv_shapes == {2} and not plan.bwd_finish and not plan.bwd_stats
+    elif name == "mha":
+        assert q_shapes == {0} and kv_shapes == {0} and not plan.bwd_finish
+    else:  # every kv shape, the row statistics pass
+        assert kv_shapes == {0, 1, 2} and plan.bwd_stats
     seq = max(lengths)
     rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)])
     b_idx, t_idx = (rows // seq).to(torch.int32), (rows % seq).to(torch.int32)
@@ -508,9 +519,39 @@ def test_packed_attention_matches_oracle(name, lengths, heads, kv_heads, dtype):
     tol = TOL[dtype]
     err = float(np.max(np.abs(out.detach().cpu().float().numpy().reshape(n, heads, 128) - o_ref)))
     assert err <= tol["o"], err
-    for name, mine, theirs in (("q", qd.grad, dq_in), ("k", kd.grad, dk_in), ("v", vd.grad, dv_in)):
+    for which, mine, theirs in (("q", qd.grad, dq_in), ("k", kd.grad, dk_in),
+                                ("v", vd.grad, dv_in)):
         r = rel(mine.cpu().float().numpy(), theirs)
-        assert r <= tol["g"], (name, r)
+        assert r <= tol["g"], (which, r)
+
+
+def test_packed_attention_device_lengths_match_host_lengths():
+    """packed_attention with the lengths as a device tensor (device cu_seqlens and plans, no host
+    read; the backward's rotary epilogues and flagged GQA sum over the device group list) gives
+    bitwise the host-lengths output and projection gradients: the two lists hold the same items."""
+    lengths, heads, kv_heads = [334, 200, 0, 100, 7], 12, 2
+    banner("packed_attention device lengths", lengths)
+    real = [x for x in lengths if x]
+    seq = max(real)
+    rows = torch.tensor([b * seq + t for b, length in enumerate(real) for t in range(length)])
+    b_idx, t_idx = (rows // seq).to(torch.int32).cuda(), (rows % seq).to(torch.int32).cuda()
+    n = rows.numel()
+    cos, sin = (t.cuda() for t in rope_tables(seq, seed=3))
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(n, heads * 128, generator=g).half().cuda()
+    k = torch.randn(n, kv_heads * 128, generator=g).half().cuda()
+    v = torch.randn(n, kv_heads * 128, generator=g).half().cuda()
+    do = torch.randn(n, heads * 128, generator=g).half().cuda()
+    res = []
+    for lens in (lengths, torch.tensor(lengths, device="cuda")):
+        leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+        out = att.packed_attention(*leaves, cos, sin, b_idx, t_idx, seq, heads, kv_heads, lens,
+                                   SCALE)
+        out.backward(do)
+        torch.cuda.synchronize()
+        res.append([out.detach()] + [t.grad for t in leaves])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
 
 
 HEAD_MASK = (1 << 12) - 1  # item word: kind << 24 | group << 21 | pair << 20 | (S-1) << 12 | head
@@ -1010,3 +1051,71 @@ def test_group_items_without_outputs_leave_exact_partials(lengths, hq, hkv, kind
     for a, b in zip(*res):
         assert not torch.isnan(a.float()).any()
         assert torch.equal(a, b)
+
+
+ROTARY_CASES = [
+    ([70, 33, 51, 1, 200], 12, 2, torch.float16, att._lib.VA_PLAN_BWD_HEADS, True),
+    ([70, 33, 51, 1, 200], 12, 2, torch.float16, att._lib.VA_PLAN_BWD_PAIRS, True),
+    ([70, 33, 51, 1, 200], 12, 2, torch.float16, att._lib.VA_PLAN_BWD_PAIRS, False),
+    ([180] * 45, 12, 2, torch.float16, att._lib.VA_PLAN_BWD_GROUPS, True),     # S = 6, 3, 2
+    ([180] * 45, 12, 2, torch.float16, att._lib.VA_PLAN_BWD_GROUPS, False),
+    ([300, 45, 1, 128], 28, 4, torch.bfloat16, att._lib.VA_PLAN_BWD_GROUPS_ALL, True),
+    ([64, 37, 50, 12], 4, 4, torch.float16, att._lib.VA_PLAN_BWD, True),         # Hq == Hkv
+]
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,dtype,kind,outputs", ROTARY_CASES)
+def test_rotary_backward_matches_oracle(lengths, hq, hkv, dtype, kind, outputs):
+    """va_bwd_rotary_stage (the inverse rotation in the backward kernels' epilogues) against the
+    oracle's backward followed by its inverse rotation (solution/attention.py:113-134), for every
+    item shape: per-head q items (their halves split the (d, d + 64) pairs), pair items, group
+    items of S < G and S = G heads, Hq == Hkv, and without outputs (rotated per-head partials
+    summed by VA_BWD_FINISH_HEADS). Tables of random frequencies; rows by document, as the
+    decoder's packed call forms them. The row statistics pass is used for one half of the cases."""
+    banner("rotary backward", len(lengths), sum(lengths), hq, hkv, dtype, kind, outputs)
+    dev = torch.device("cuda")
+    lib = att.lib()
+    n = sum(lengths)
+    seq = max(lengths)
+    rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)])
+    b_idx, t_idx = (rows // seq).to(torch.int32), (rows % seq).to(torch.int32)
+    cos, sin = rope_tables(seq, seed=hq + n)
+    tab, keep = att.rotary_tables(cos.to(dev), sin.to(dev), b_idx.to(dev), t_idx.to(dev))
+    cu = orc.cu_seqlens_from_lengths(lengths)
+    items = torch.from_numpy(att.build_plan_host(cu, hq, hkv, kind)).to(dev)
+    fwd = torch.from_numpy(att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_FWD)).to(dev)
+    q, k, v, do = wl.make_inputs(lengths, hq, hkv, dtype, seed=n + hq)
+    qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
+    code = att._lib.VA_F16 if dtype == torch.float16 else att._lib.VA_BF16
+    out = torch.empty_like(qd)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+    att.check(lib.va_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                         lse.data_ptr(), fwd.data_ptr(), fwd.shape[0], n, hq, hkv, 128, SCALE, code,
+                         att._stream()), "va_fwd")
+    ws = att.bwd_workspace(n, hq, hkv, dev)[0]
+    dq = torch.full_like(qd, float("nan"))
+    dk, dv = torch.full_like(kd, float("nan")), torch.full_like(vd, float("nan"))
+    stats = len(lengths) % 2 == 1
+
+    def argv(with_out):
+        return (dod.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                lse.data_ptr(), items.data_ptr(), items.shape[0], n, hq, hkv, 128, SCALE, code,
+                dq.data_ptr(), dk.data_ptr() if with_out else None,
+                dv.data_ptr() if with_out else None, ws.data_ptr(), ws.numel(), att._stream())
+    if stats:
+        att.check(lib.va_bwd_rotary_stage(att._lib.VA_BWD_STATS, ctypes.byref(tab), *argv(outputs)),
+                  "va_bwd_rotary_stage")
+    main = att._lib.VA_BWD_MAIN_STATS if stats else att._lib.VA_BWD_MAIN
+    att.check(lib.va_bwd_rotary_stage(main, ctypes.byref(tab), *argv(outputs)),
+              "va_bwd_rotary_stage")
+    if hq != hkv:
+        finish = att._lib.VA_BWD_FINISH if outputs else att._lib.VA_BWD_FINISH_HEADS
+        att.check(lib.va_bwd_stage(finish, *argv(True)), "va_bwd_stage")
+    torch.cuda.synchronize()
+    o_ref, _lse, dq_ref, dk_ref, dv_ref = oracle(q, k, v, do, lengths)
+    refs = (orc.rope_backward(dq_ref, cos.numpy(), sin.numpy(), b_idx, t_idx).reshape(n, hq, 128),
+            orc.rope_backward(dk_ref, cos.numpy(), sin.numpy(), b_idx, t_idx).reshape(n, hkv, 128),
+            dv_ref)
+    for which, mine, ref in zip("qkv", (dq, dk, dv), refs):
+        r = rel(mine.cpu().float().numpy(), ref)
+        assert r <= TOL[dtype]["g"], (which, r)
