@@ -177,7 +177,7 @@ int va_bwd(const void* dout, const void* q, const void* k, const void* v, const 
 /* The same backward for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. Same inputs and outputs as va_bwd, no workspace: the dK/dV partials live in a static
- * device array of the library (va_bwd_noalloc_max_bytes() = 65 MiB per GPU, held until the
+ * device array of the library (va_bwd_noalloc_max_bytes() = 66 MiB per GPU, held until the
  * process ends: partials and row flags), so total_tokens * Hq must not exceed 131072 at head_dim 128 (VA_ECAPACITY
  * otherwise, before any launch); dk and dv must be given. Calls nothing that allocates. Calls
  * that overlap on one GPU (two streams or two threads) race on the shared array. */

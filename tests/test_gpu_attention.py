@@ -279,19 +279,31 @@ def test_benchmark_configs_match_oracle(cfg):
     check_all(out, grads, oracle(q, k, v, do, lengths), dtype, sum(lengths), c["hq"])
 
 
+def config5_checked_documents(lengths):
+    """Documents of configuration 5 checked against the oracle: one at every length decile (the
+    shortest, the 10th, ..., 90th percentile and the longest), the three longest, the first and
+    the last."""
+    order = sorted(range(len(lengths)), key=lambda i: lengths[i])
+    deciles = [order[min(len(order) - 1, (len(order) - 1) * p // 10)] for p in range(11)]
+    return sorted(set(deciles + order[-3:] + [0, len(lengths) - 1]))
+
+
 def test_7b_config_documents_match_oracle():
-    """Configuration 5 (7B heads, 67 documents up to 1740 tokens) at full size on the GPU,
-    checked against the oracle on every query and key/value head of six documents: the three
-    longest, the first, the last and the shortest."""
+    """Configuration 5 (7B heads, 67 documents up to 1740 tokens) at full size on the GPU (the
+    group-item backward list and the row statistics pass, as the benchmark runs it), checked
+    against the oracle on every query and key/value head of one document per length decile, the
+    three longest, the first and the last."""
     lengths = wl.config_lengths(5)
     c = wl.CONFIGS[5]
     dtype = wl.torch_dtype(c["dtype"])
     banner("config", 5, len(lengths), sum(lengths))
+    plan = att._plan(att._cu_seqlens(lengths, torch.device("cuda")), c["hq"], c["hkv"])
+    assert plan.bwd_stats and not plan.bwd_finish
     q, k, v, do = wl.make_inputs(lengths, c["hq"], c["hkv"], dtype, seed=0)
     out, dq, dk, dv = run_varlen(q, k, v, do, lengths)
     cu = orc.cu_seqlens_from_lengths(lengths)
-    order = sorted(range(len(lengths)), key=lambda i: -lengths[i])
-    docs = sorted(set(order[:3] + [0, len(lengths) - 1, order[-1]]))
+    docs = config5_checked_documents(lengths)
+    assert len(docs) >= 11
     o_all = out.reshape(-1, c["hq"], 128)
     for d in docs:
         s, e = int(cu[d]), int(cu[d + 1])
