@@ -422,26 +422,32 @@ def rotary_tables(cos, sin, b_idx, t_idx):
 def rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads, out_dtype, layout=0,
                  expand=False, batch=0, seq=0):
     """Rotated q, k and cast v as three tensors of `out_dtype`, in the packed (N, H, D) or the
-    zero-filled padded (B, H, T, D) layout; K/V keep kv_heads unless `expand`."""
+    zero-filled padded (B, H, T, D) layout; K/V keep kv_heads unless `expand`. A packed,
+    unexpanded v already in `out_dtype` is returned as a view of itself (the kernel leaves the
+    value rows out)."""
     _require_device(q, k, v, cos, sin, b_idx, t_idx)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     cos, sin = _tables(cos, sin)
     n = q.shape[0]
     kvo = heads if expand else kv_heads
+    if q.shape[1] != heads * HEAD_DIM or k.shape[1] != kv_heads * HEAD_DIM or v.shape != k.shape:
+        raise ValueError("projection shapes do not match heads * head_dim")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q, k and v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    v_as_is = layout == _lib.VA_LAYOUT_PACKED and not expand and v.dtype == out_dtype
     if layout == _lib.VA_LAYOUT_PADDED:
         qo = torch.zeros(batch, heads, seq, HEAD_DIM, dtype=out_dtype, device=q.device)
         ko, vo = torch.zeros_like(qo), torch.zeros_like(qo)
     else:
         qo = torch.empty(n, heads, HEAD_DIM, dtype=out_dtype, device=q.device)
         ko = torch.empty(n, kvo, HEAD_DIM, dtype=out_dtype, device=q.device)
-        vo = torch.empty_like(ko)
-    if q.shape[1] != heads * HEAD_DIM or k.shape[1] != kv_heads * HEAD_DIM or v.shape != k.shape:
-        raise ValueError("projection shapes do not match heads * head_dim")
+        vo = v.view(n, kv_heads, HEAD_DIM) if v_as_is else torch.empty_like(ko)
     scb, sct = _rope_strides(cos)
-    check(lib().va_rope_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(cos), _ptr(sin), scb, sct,
-                            _ptr(b_idx), _ptr(t_idx), _ptr(qo), _ptr(ko), _ptr(vo), n, heads,
-                            kv_heads, HEAD_DIM, seq, _DTYPES[q.dtype], _DTYPES[out_dtype], layout,
-                            int(expand), _stream()), "va_rope_fwd")
+    check(lib().va_rope_fwd(_ptr(q), _ptr(k), None if v_as_is else _ptr(v), _ptr(cos), _ptr(sin),
+                            scb, sct, _ptr(b_idx), _ptr(t_idx), _ptr(qo), _ptr(ko),
+                            None if v_as_is else _ptr(vo), n, heads, kv_heads, HEAD_DIM, seq,
+                            _DTYPES[q.dtype], _DTYPES[out_dtype], layout, int(expand), _stream()),
+          "va_rope_fwd")
     return qo, ko, vo
 
 

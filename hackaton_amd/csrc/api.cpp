@@ -4,6 +4,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 
 #include "../../include/varlen_attn.h"
 #include "va_api_internal.h"
@@ -240,14 +241,24 @@ int rope_common(const void* x0, const void* x1, const void* x2, const float* cos
   if (layout == VA_LAYOUT_PADDED && (seq <= 0 || !expand))
     return va::fail(VA_EINVAL, "%s: padded layout needs seq > 0 and expand = 1", what);
   if (n_tokens == 0) return VA_OK;
-  for (const void* p : {x0, x1, x2, (const void*)cos, (const void*)sin, (const void*)b_idx,
-                        (const void*)t_idx, (const void*)y0, (const void*)y1, (const void*)y2}) {
+  // The value rows may be left out (both pointers NULL) of a forward that expands nothing: v then
+  // needs neither rotation nor expansion, and a caller whose v is already in out_dtype uses it as
+  // it is.
+  const bool no_v = x2 == nullptr && y2 == nullptr;
+  if (no_v && (expand || std::strcmp(what, "va_rope_fwd") != 0))
+    return va::fail(VA_EINVAL, "%s: the value rows may only be left out of va_rope_fwd without "
+                               "expand", what);
+  for (const void* p : {x0, x1, (const void*)cos, (const void*)sin, (const void*)b_idx,
+                        (const void*)t_idx, (const void*)y0, (const void*)y1}) {
     if (p == nullptr) return va::fail(VA_EINVAL, "%s: NULL buffer", what);
   }
+  if (!no_v && (x2 == nullptr || y2 == nullptr))
+    return va::fail(VA_EINVAL, "%s: NULL buffer", what);
   // 16-byte lane accesses: tensor bases and the cos/sin row starts must be 16-byte aligned.
   for (const void* p : {x0, x1, x2, (const void*)cos, (const void*)sin, (const void*)y0,
                         (const void*)y1, (const void*)y2}) {
-    if (!aligned16(p)) return va::fail(VA_EINVAL, "%s: buffer not 16-byte aligned", what);
+    if (p != nullptr && !aligned16(p))
+      return va::fail(VA_EINVAL, "%s: buffer not 16-byte aligned", what);
   }
   return VA_OK;
 }

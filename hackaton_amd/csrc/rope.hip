@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_fwd_kernel(RopeArgs a) {
   const long pid = tl.pid;
   const int c0 = 8 * tl.j;
   const int b = a.b_idx[pid], t = a.t_idx[pid];
-  const int slots = a.heads + 2 * a.kv_heads;
+  const int slots = a.heads + (a.x2 != nullptr ? 2 : 1) * a.kv_heads;  // no value rows: x2 null
   for (int s0 = tl.r0; s0 < slots; s0 += 16) {
     const int s1 = s0 + 8;
     const RowIn<IN> u = fwd_load<IN>(a, pid, c0, s0);

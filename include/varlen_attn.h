@@ -239,6 +239,8 @@ int va_bwd_rotary_stage(int32_t stage, const va_rope_tables* rope, const void* d
  * Rotation in fp32, rounded once to out_dtype. layout VA_LAYOUT_PACKED writes (N, H, D),
  * VA_LAYOUT_PADDED writes (B, H, seq, D) (caller zero-fills). expand=1 writes K/V for all `heads`
  * (reference qkv_rotate semantics); expand=0 keeps kv_heads (GQA-native attention input).
+ * v and v_out may both be NULL in a forward without expand: only the q and k rows are written
+ * (for a caller whose v is already in out_dtype and uses it as it is).
  * Backward: the inverse rotation (and the sum of the G copies when expand=1); dq/dk/dv read in
  * in_dtype from `layout`, written (N, H*D) in out_dtype. Every tensor base must be 16-byte aligned
  * and the cos/sin strides (in elements) non-negative multiples of 4: each lane moves 16 bytes.

@@ -420,3 +420,21 @@ def test_row_statistics_rule():
         assert bwd_row_stats(np.concatenate([[0], np.cumsum(lengths)])) is expect, cfg
     use = ctypes.c_int32(7)
     assert _lib.lib().va_plan_bwd_row_stats(None, 1, ctypes.byref(use)) == _lib.VA_EINVAL
+
+
+def test_rope_forward_may_leave_the_value_rows_out_only_without_expand():
+    """va_rope_fwd takes v = v_out = NULL (value rows left out: the caller uses its v as it is)
+    only when nothing is expanded; the backward always needs dv. Checked before any launch."""
+    lib = _lib.lib()
+    f = ctypes.c_void_p(0x1000)
+
+    def call(fn, v, v_out, expand):
+        # (x0, x1, x2, cos, sin, strides, b_idx, t_idx, y0, y1, y2, n, heads, kv_heads, D, seq,
+        #  in_dtype, out_dtype, layout, expand, stream)
+        return fn(f, f, v, f, f, 0, 128, f, f, f, f, v_out, 10, 12, 2, 128, 0, 0, 0, 0, expand,
+                  None)
+    rc = call(lib.va_rope_fwd, None, None, 1)
+    assert rc == _lib.VA_EINVAL and b"left out" in lib.va_last_error()  # expand = 1
+    assert call(lib.va_rope_fwd, f, None, 0) == _lib.VA_EINVAL  # only one of the two
+    rc = call(lib.va_rope_bwd, None, None, 0)
+    assert rc == _lib.VA_EINVAL and b"left out" in lib.va_last_error()

@@ -1131,3 +1131,37 @@ def test_rotary_backward_matches_oracle(lengths, hq, hkv, dtype, kind, outputs):
     for which, mine, ref in zip("qkv", (dq, dk, dv), refs):
         r = rel(mine.cpu().float().numpy(), ref)
         assert r <= TOL[dtype]["g"], (which, r)
+
+
+def test_rope_forward_passes_v_through_when_it_needs_no_cast():
+    """The packed rotation without expansion leaves the value rows out of the kernel when v is
+    already in the compute type (v is returned as a view of itself); q and k come out bitwise as
+    when the kernel also casts v (an fp32 v)."""
+    lengths, heads, kv_heads = [70, 33, 200], 12, 2
+    banner("rope forward, v as it is", lengths)
+    seq = max(lengths)
+    rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)])
+    b_idx, t_idx = ((rows // seq).to(torch.int32).cuda(), (rows % seq).to(torch.int32).cuda())
+    n = rows.numel()
+    cos, sin = (t.cuda() for t in rope_tables(seq, seed=4))
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(n, heads * 128, generator=g).half().cuda()
+    k = torch.randn(n, kv_heads * 128, generator=g).half().cuda()
+    v = torch.randn(n, kv_heads * 128, generator=g).half().cuda()
+    qa, ka, va = att.rope_forward(q, k, v, cos, sin, b_idx, t_idx, heads, kv_heads,
+                                  torch.float16)
+    # the same rotation with the value rows copied by the kernel
+    qb, kb = torch.empty_like(qa), torch.empty_like(ka)
+    vb = torch.empty(n, kv_heads, 128, dtype=torch.float16, device="cuda")
+    tab_cos, tab_sin = cos.float().contiguous(), sin.float().contiguous()
+    att.check(att.lib().va_rope_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), tab_cos.data_ptr(),
+                                    tab_sin.data_ptr(), 0, 128, b_idx.data_ptr(),
+                                    t_idx.data_ptr(), qb.data_ptr(), kb.data_ptr(),
+                                    vb.data_ptr(), n, heads, kv_heads, 128, 0, 0, 0, 0, 0,
+                                    att._stream()), "va_rope_fwd")
+    torch.cuda.synchronize()
+    assert va.data_ptr() == v.data_ptr() and va.shape == (n, kv_heads, 128)
+    assert torch.equal(qa, qb) and torch.equal(ka, kb)
+    assert torch.equal(va, vb) and torch.equal(vb.reshape(n, -1), v)
+    with pytest.raises(ValueError, match="share a dtype"):
+        att.rope_forward(q, k, v.float(), cos, sin, b_idx, t_idx, heads, kv_heads, torch.float16)
