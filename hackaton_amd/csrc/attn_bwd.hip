@@ -732,20 +732,46 @@ __device__ __forceinline__ void bwd_q_item(
   }
 
   if (pair) {
-    if constexpr (ROPE) {  // dQ back to the projection's frame, in place (next tables ahead)
+    if constexpr (ROPE) {  // dQ back to the projection's frame, in place
+      // The two halves hold the same 32 rows of their strip (heads h and h + 1): each loads the
+      // tables of two of the four accumulators' d ranges and both read all four back from LDS
+      // (free after the loop's last barrier), so each table row is read once per item.
+      lds_f32x4* xt = reinterpret_cast<lds_f32x4*>(
+          (__attribute__((address_space(3))) float*)(smem));
+      auto tslot = [&](int db, int m) { return ((strip * 4 + db) * 8 + m) * 64 + lane; };
+      static_assert(NS * 4 * 8 * 64 * 16 <= HALFS * 2, "rotary tables fit in LDS");
       const int trow = trow_lds[tid];
-      Tab8 t0 = load_tab8(rope, trow, 8 * hi), t1;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int db = 2 * half + j;
+        const Tab8 t = load_tab8(rope, trow, 16 * db + 8 * hi);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          xt[tslot(db, i)] = t.c1[i];
+          xt[tslot(db, 2 + i)] = t.c2[i];
+          xt[tslot(db, 4 + i)] = t.s1[i];
+          xt[tslot(db, 6 + i)] = t.s2[i];
+        }
+      }
+      __syncthreads();
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        if (db + 1 < 4) t1 = load_tab8(rope, trow, 16 * (db + 1) + 8 * hi);
+        Tab8 t;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          t.c1[i] = xt[tslot(db, i)];
+          t.c2[i] = xt[tslot(db, 2 + i)];
+          t.s1[i] = xt[tslot(db, 4 + i)];
+          t.s2[i] = xt[tslot(db, 6 + i)];
+        }
         float x[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) x[i] = dqacc[db][i];
-        rope_unrotate8(t0, x);
+        rope_unrotate8(t, x);
 #pragma unroll
         for (int i = 0; i < 16; ++i) dqacc[db][i] = x[i];
-        t0 = t1;
       }
+      __syncthreads();  // every wave has its tables before the row tiles reuse the LDS
     }
     // Each half holds its head's whole dQ^T: 64 columns at a time through this wave's own row
     // tile (the LDS is free after the loop's last barrier), scaled.

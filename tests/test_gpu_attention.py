@@ -537,12 +537,17 @@ def test_packed_attention_matches_oracle(name, lengths, heads, kv_heads, dtype):
         assert r <= tol["g"], (which, r)
 
 
-def test_packed_attention_device_lengths_match_host_lengths():
+@pytest.mark.parametrize("lengths", [[334, 200, 0, 100, 7], wl.config_lengths(3)[:30] + [0]])
+def test_packed_attention_device_lengths_match_host_lengths(lengths):
     """packed_attention with the lengths as a device tensor (device cu_seqlens and plans, no host
-    read; the backward's rotary epilogues and flagged GQA sum over the device group list) gives
-    bitwise the host-lengths output and projection gradients: the two lists hold the same items."""
-    lengths, heads, kv_heads = [334, 200, 0, 100, 7], 12, 2
-    banner("packed_attention device lengths", lengths)
+    read) gives bitwise the host-lengths output and projection gradients: the two lists hold the
+    same items. Short lists take the partials route and the inverse rotation pass; the 30
+    documents of configuration 3 (ceil(N / 128) Hq >= 512) the rotary epilogues and the flagged
+    GQA sum over the group list."""
+    heads, kv_heads = 12, 2
+    banner("packed_attention device lengths", len(lengths), sum(lengths))
+    n_real = sum(lengths)
+    assert att.rotary_epilogues(n_real, heads) == (len(lengths) > 5)
     real = [x for x in lengths if x]
     seq = max(real)
     rows = torch.tensor([b * seq + t for b, length in enumerate(real) for t in range(length)])
