@@ -947,8 +947,11 @@ __global__ __launch_bounds__(bwd::NT, 1) void bwd_kernel(
 // Row statistics of the backward, once per (query head, row): {lse log2 e, delta = rowsum(dO * O)}
 // in fp32, with the arithmetic of the items' own staging (16 threads per row, v_dot2 over each
 // thread's 8 elements, then the 16-lane DPP sum), so that the main kernel's results do not depend
-// on where delta was formed. Rows are taken in memory order (token-major, all heads of a token
-// are adjacent), 64 per work-group, 4 per thread (8 loads in flight each).
+// on where delta was formed. Rows are taken in the statistics' own (head, token) order, 64 per
+// work-group, 4 per thread (8 loads of O / dO and 4 of lse in flight each): lse is read and the
+// statistics written as whole lines, while each O / dO row is a contiguous 256 bytes anyway. In
+// the token-major order of O / dO the 8-byte statistics of one line came from several
+// work-groups (config 5: 98-100 us against 92).
 // --------------------------------------------------------------------------------------------
 constexpr int kStatThreads = 256, kStatRows = 64;
 template <class E>
@@ -961,9 +964,13 @@ __global__ __launch_bounds__(kStatThreads) void bwd_stats_kernel(
   const int col = 8 * (tid & 15);
   constexpr int R = kStatRows / (kStatThreads / 16);
   u32x4 o[R], g[R];
+  float l[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const long at = min(r0 + 16 * i, rows - 1) * kHeadDim + col;
+    const long r = min(r0 + 16 * i, rows - 1);  // h * n_tokens + token
+    const int h = (int)(r / n_tokens), token = (int)(r - (long)h * n_tokens);
+    const long at = ((long)token * hq + h) * kHeadDim + col;
+    l[i] = lse[r];
     o[i] = gload16(out + at);
     g[i] = gload16(dout + at);
   }
@@ -974,11 +981,7 @@ __global__ __launch_bounds__(kStatThreads) void bwd_stats_kernel(
     for (int w = 0; w < 4; ++w) d = E::dot2(o[i][w], g[i][w], d);
     d = sum_rows16(d);
     const long r = r0 + 16 * i;
-    if ((tid & 15) == 0 && r < rows) {
-      const int token = (int)(r / hq), h = (int)(r - (long)token * hq);
-      const long at = (long)h * n_tokens + token;
-      stats[at] = f32x2{lse[at] * kLog2e, d};
-    }
+    if ((tid & 15) == 0 && r < rows) stats[r] = f32x2{l[i] * kLog2e, d};
   }
 }
 
