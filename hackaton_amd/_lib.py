@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvarlen_a
 VA_OK, VA_EINVAL, VA_ESHAPE, VA_EDTYPE, VA_ESEQ, VA_ECAPACITY = 0, -1, -2, -3, -4, -5
 VA_F16, VA_BF16, VA_F32 = 0, 1, 2
 VA_PLAN_FWD, VA_PLAN_BWD, VA_PLAN_BWD_HEADS, VA_PLAN_BWD_PAIRS = 0, 1, 2, 3
-VA_PLAN_BWD_GROUPS, VA_PLAN_BWD_GROUPS_ALL = 4, 5
+VA_PLAN_BWD_GROUPS, VA_PLAN_BWD_GROUPS_ALL, VA_PLAN_FWD_NARROW = 4, 5, 6
 VA_BWD_PAIR_MIN_ITEMS = 1024
 VA_LAYOUT_PACKED, VA_LAYOUT_PADDED = 0, 1
 VA_BWD_MAIN, VA_BWD_FINISH, VA_BWD_FINISH_HEADS, VA_BWD_STATS, VA_BWD_MAIN_STATS = 1, 2, 3, 4, 5

@@ -90,7 +90,8 @@ def _cu_seqlens(lengths, device):
 
 class Plan:
     """Device work lists of the forward and backward kernels for one (cu_seqlens, Hq, Hkv). The
-    backward list takes GQA group items where they do not lengthen it (VA_PLAN_BWD_GROUPS); a
+    forward list splits its longest items into narrow ones where it is short (VA_PLAN_FWD_NARROW);
+    the backward list takes GQA group items where they do not lengthen it (VA_PLAN_BWD_GROUPS); a
     backward that leaves per-head dK/dV partials to its caller takes `partial_bwd()`, the list
     without them."""
 
@@ -103,7 +104,8 @@ class Plan:
         self.total = int(cu[-1])
         self._hq, self._hkv = hq, hkv
         bwd_kind = _lib.VA_PLAN_BWD_GROUPS if hq > hkv else _lib.VA_PLAN_BWD
-        host_fwd = build_plan_host(cu, hq, hkv, _lib.VA_PLAN_FWD)
+        # the forward list with its longest items split in two where it leaves CUs idle
+        host_fwd = build_plan_host(cu, hq, hkv, _lib.VA_PLAN_FWD_NARROW)
         host_bwd = build_plan_host(cu, hq, hkv, bwd_kind)
         self.n_fwd, self.n_bwd = host_fwd.shape[0], host_bwd.shape[0]
         self.fwd_items = torch.from_numpy(host_fwd).to(device)
@@ -159,7 +161,8 @@ def build_plan_host(cu, hq, hkv, kind):
 
 class DevicePlan:
     """Work lists and cu_seqlens built on the device from device lengths: no host read. One launch
-    (va_plan_build_device_lengths) builds cu_seqlens, the forward list and the backward list
+    (va_plan_build_device_lengths) builds cu_seqlens, the forward list (VA_PLAN_FWD_NARROW, as the
+    host plan's) and the backward list
     without GQA group items; with Hq > Hkv a second (va_plan_build_device from that cu_seqlens)
     builds the backward list with them (VA_PLAN_BWD_GROUPS), and the first one serves a backward
     that leaves per-head partials to its caller. Each list has the capacity that the host-known
@@ -177,7 +180,7 @@ class DevicePlan:
         self.total = int(n_tokens)
         dev = lengths.device
         caps = []
-        for kind in (_lib.VA_PLAN_FWD, _lib.VA_PLAN_BWD):
+        for kind in (_lib.VA_PLAN_FWD_NARROW, _lib.VA_PLAN_BWD):
             cap = np.zeros(1, dtype=np.int64)
             check(lib().va_plan_capacity(n_tokens, n_docs, hq, kind, cap.ctypes.data_as(_lib._pi64)),
                   "va_plan_capacity")

@@ -39,6 +39,259 @@ static_assert(NT == 512 && BN == 64, "pair copy map: 2 groups of 4 rows per wave
 static_assert(BM == kFwdBlockM, "the plan's query tile");
 }  // namespace fwd
 
+// --------------------------------------------------------------------------------------------
+// Narrow item of the 8-wave forward (kItemNarrowBit): 64 queries of one head, 8 waves = 2 query
+// strips x 4 key phases (wave w: strip w & 1, phase w >> 1). The keys go in quads of 128, the
+// K and V of a 64-key tile pair copied into a stage as a wide item's pairs are (K0, V0, K1, V1);
+// phase j takes the quad's 32-key tile j (rows 32 (j & 1) of the pair's tile j >> 1). A wave
+// then walks a quarter of the item's keys, half as many quads as a wide item's waves walk tile
+// pairs, with half a pair's MFMA work in each: the plan gives its longest items this shape when
+// the list leaves CUs idle. At the end the four phases of a strip merge (m, l, O) through LDS
+// and phase j finishes the 32 columns [32 j, 32 j + 32) of its strip.
+// --------------------------------------------------------------------------------------------
+template <class E>
+__device__ __forceinline__ void fwd_narrow_item(
+    lds_u16* smem, uint16_t* smem_raw, int q0, int doc_end, int doc_start, int h,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, int hq, int hkv, uint16_t* __restrict__ o,
+    float* __restrict__ lse, int n_tokens, float scale_log2) {
+  using namespace fwd;
+  const int group = hq / hkv;
+  const int kvh = h / group;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int strip = wave & 1, phase = wave >> 1;
+  const int src = lane & 15, grp = lane >> 4;
+  const long qrow = (long)hq * D, kvrow = (long)hkv * D;
+  const int wq0 = q0 + 32 * strip;
+  const int my_q = wq0 + l32;
+  const bool q_valid = my_q < doc_end;
+  const int ws = __builtin_amdgcn_readfirstlane(wave);
+  const int wq0_u = __builtin_amdgcn_readfirstlane(wq0);
+  const int kv_end = min(q0 + 64, doc_end);
+  const int n_quads = (kv_end - doc_start + 2 * BN - 1) / (2 * BN);
+
+  // Copies (straight from HBM into LDS, swizzled rows as in the wide item): every wave moves row
+  // groups 2 w and 2 w + 1 (4 rows each) of each 64-row tile, 8 instructions per quad; rows past
+  // the document end read as zeros.
+  int coff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 4 * (2 * wave + j) + (lane >> 4);
+    coff[j] = (r * (int)kvrow + 8 * ((lane & 15) ^ swz16(r))) * 2;
+  }
+  auto copy_tile = [&](int t, int x, uint32_t dst) {  // 64-key tile t of K (x = 0) or V
+    const int row0 = doc_start + t * BN;
+    const long base = (long)row0 * kvrow + kvh * D;
+    const long bytes = ((long)(doc_end - row0 - 1) * kvrow + D) * 2;
+    const u32x4 r = make_rsrc4((x ? v : k) + base, bytes);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16_opaque(r, dst + 4 * (2 * ws + j) * D * 2, coff[j]);
+  };
+  auto copy_quad = [&](int p, int stage) {
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr(smem + stage * PAIR));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) copy_tile(2 * p + (i >> 1), i & 1, dst + i * TILE * 2);
+  };
+
+  int koff[8], toff[4][2];
+  {
+    const int r = perm32(l32), f = swz16(r);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) koff[kk] = r * D + 8 * ((2 * kk + hi) ^ f);
+    const int sg = (((src & 3) & 1) << 1) | ((src & 3) >> 1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int rr = 8 * hi + 2 * (src >> 2) + e;
+        const int lc = 2 * (grp & 1) + 4 * db + (sg >> 1);
+        toff[db][e] = rr * D + 8 * (lc ^ swz16(rr)) + 4 * (sg & 1);
+      }
+  }
+
+  u32x4 qf[8];
+  f32x16 oacc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // S^T of the phase's 32-key tile (K rows at `kb`): 8 MFMAs, K operands read 4 ahead.
+  auto s_blk = [&](const lds_u16* kb, f32x16& s) {
+    s = f32x16{};
+    u32x4 ka[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ka[i] = ld128(kb + koff[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s = E::mfma(ka[i & 3], qf[i], s);
+      if (i + 4 < 8) ka[i & 3] = ld128(kb + koff[i + 4]);
+    }
+  };
+  // Mask, online softmax and O^T += V^T P^T of the tile (V rows at `vb`, keys from kv0).
+  auto pv_blk = [&](const lds_u16* vb, int kv0, f32x16& s) {
+    auto v_read = [&](int i) {  // i = (c, db): keys 16 c .. 16 c + 15, d block db
+      const lds_u16* p = vb + 16 * (i >> 2) * D;
+      const u32x2 x = ldtr(p + toff[i & 3][0]), y = ldtr(p + toff[i & 3][1]);
+      return u32x4{x[0], x[1], y[0], y[1]};
+    };
+    u32x4 va[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = v_read(i);
+    if (kv0 + 31 > wq0_u) {  // the tile crosses this strip's diagonal: key > query -> -inf
+      const int lim = my_q - kv0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (reg_row(j, hi) > lim) s[j] = -INFINITY;
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mt = fmaxf(mt, s[j]);
+    mt = max_with_other_half(mt) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) oacc[db] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float rs = 0.f;
+    u32x4 pf[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(s[8 * c + e], scale_log2, -m_use));
+      pf[c] = pack8_tr<E>(p);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) rs = E::sum2(pf[c][w], rs);
+    }
+    l_run += rs;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      oacc[i & 3] = E::mfma(va[i & 3], pf[i >> 2], oacc[i & 3]);
+      if (i + 4 < 8) va[i & 3] = v_read(i + 4);
+    }
+  };
+
+  // Q of the 64 queries into the second stage (every wave 2 row groups of 4 rows), quad 0 into
+  // the first; every lane reads its query's row back as its B operand.
+  {
+    const long bytes = ((long)(doc_end - q0 - 1) * qrow + (long)(h + 1) * D) * 2;
+    const u32x4 rq = make_rsrc4(q + (long)q0 * qrow, bytes);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 4 * (2 * wave + j) + (lane >> 4);
+      dma16_opaque(rq, lds_addr(smem + PAIR + 4 * (2 * ws + j) * D),
+                   (r * (int)qrow + h * D + 8 * ((lane & 15) ^ swz16(r))) * 2);
+    }
+  }
+  copy_quad(0, 0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  {
+    const int r = 32 * strip + l32, f = swz16(r);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = ld128(smem + PAIR + r * D + 8 * ((2 * kk + hi) ^ f));
+  }
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) settle(qf[kk]);
+  __syncthreads();  // every wave holds its Q before the loop overwrites the second stage
+  const bool strip_live = wq0_u < doc_end;
+  const int ph = __builtin_amdgcn_readfirstlane(phase);
+  for (int p = 0; p < n_quads; ++p) {
+    const int stage = p & 1;
+    const int kv0 = doc_start + 32 * (4 * p + ph);
+    const lds_u16* kb = smem + stage * PAIR + (ph >> 1) * 2 * TILE + 32 * (ph & 1) * D;
+    if (strip_live && kv0 < kv_end && kv0 <= wq0_u + 31) {
+      f32x16 s;
+      s_blk(kb, s);
+      if (p + 1 < n_quads) copy_quad(p + 1, stage ^ 1);
+      pv_blk(kb + TILE, kv0, s);
+    } else if (p + 1 < n_quads) {
+      copy_quad(p + 1, stage ^ 1);
+    }
+    wait_vmcnt<0>();  // this wave's copies of the next quad have landed in LDS
+    __syncthreads();
+  }
+
+  // Merge of the four phases of each strip (the stages are free after the last barrier): phase
+  // j sends its partial O of the other phases' columns (16-byte chunks, same lane order) and
+  // publishes (m, l); phase J then finishes d in [32 J, 32 J + 32), the phases' terms added in
+  // phase order.
+  lds_f32x4* xo = reinterpret_cast<lds_f32x4*>((__attribute__((address_space(3))) float*)(smem));
+  constexpr int kSlots = 2 * 4 * 3 * 4 * 64;  // [strip][dst][src, dst left out][j4][lane]
+  float* xs = reinterpret_cast<float*>(smem_raw) + kSlots * 4;  // [strip][phase][m | l][lane]
+  static_assert((kSlots * 4 + 2 * 4 * 2 * 64) * 4 <= 2 * PAIR * 2, "narrow merge fits in LDS");
+  auto xslot = [&](int dst, int from, int j4) {
+    return (((strip * 4 + dst) * 3 + from - (from > dst ? 1 : 0)) * 4 + j4) * 64 + lane;
+  };
+  auto merge = [&](auto phase_c) {
+    constexpr int J = decltype(phase_c)::value;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      if (db == J) continue;
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4)
+        xo[xslot(db, J, j4)] = f32x4{oacc[db][4 * j4], oacc[db][4 * j4 + 1],
+                                     oacc[db][4 * j4 + 2], oacc[db][4 * j4 + 3]};
+    }
+    xs[((strip * 4 + J) * 2 + 0) * 64 + lane] = m_run;
+    xs[((strip * 4 + J) * 2 + 1) * 64 + lane] = l_run;
+    __syncthreads();
+    float mk[4], lk[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      mk[f] = xs[((strip * 4 + f) * 2 + 0) * 64 + lane];
+      lk[f] = xs[((strip * 4 + f) * 2 + 1) * 64 + lane];
+    }
+    const float m_tot = fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3]));
+    const float m_use = m_tot == -INFINITY ? 0.f : m_tot;
+    float sk[4], lsum = 0.f;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      sk[f] = fast_exp2(mk[f] - m_use);
+      lsum += lk[f] * sk[f];
+    }
+    const float l_tot = sum_with_other_half(lsum);
+    const float inv = 1.f / l_tot;
+    float x[16];
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const f32x4 y = f == J ? f32x4{oacc[J][4 * j4], oacc[J][4 * j4 + 1], oacc[J][4 * j4 + 2],
+                                       oacc[J][4 * j4 + 3]}
+                               : xo[xslot(J, f, j4)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += y[e] * sk[f];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * j4 + e] = acc[e] * inv;
+    }
+    u32x4 w[2];  // chunk c: d = 32 J + 16 c + 8 hi + 0..7 of query wq0 + l32
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      w[c] = pack8<E>(x[8 * c], x[8 * c + 1], x[8 * c + 2], x[8 * c + 3], x[8 * c + 4],
+                      x[8 * c + 5], x[8 * c + 6], x[8 * c + 7]);
+    // Whole 64-byte row runs through this wave's own exchange slots (read above by this wave
+    // only) as an LDS row tile.
+    store_rows32<4>(reinterpret_cast<lds_u16*>(&xo[(strip * 4 + J) * 3 * 4 * 64]), w, lane,
+                    [&](int r) { return o + (long)(wq0 + r) * qrow + h * D + 32 * J; },
+                    doc_end - wq0);
+    if (J == 0 && q_valid && hi == 0)
+      __builtin_nontemporal_store((m_tot + fast_log2(l_tot)) * kLn2, &lse[(long)h * n_tokens + my_q]);
+  };
+  switch (ph) {
+    case 0: merge(std::integral_constant<int, 0>{}); break;
+    case 1: merge(std::integral_constant<int, 1>{}); break;
+    case 2: merge(std::integral_constant<int, 2>{}); break;
+    default: merge(std::integral_constant<int, 3>{}); break;
+  }
+}
+
 template <class E>
 // Arguments in the order the work-group needs them: the first 14 dwords are preloaded into
 // SGPRs at launch (-amdgpu-kernarg-preload-count), so the work item's load starts at once.
@@ -51,11 +304,17 @@ __global__ __launch_bounds__(fwd::NT, 1) void fwd_kernel(
   lds_u16* smem = (lds_u16*)smem_raw;
 
   const int4 it = items[blockIdx.x];
-  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w;
+  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kItemHeadMask;
   // Empty slots of a device-built plan, and items that do not fit this launch (a plan built for
   // other sizes), are skipped: nothing outside [0, n_tokens) x [0, hq) is ever addressed.
-  if (q0 >= doc_end || doc_start < 0 || q0 < doc_start || doc_end > n_tokens || h < 0 || h >= hq)
+  if ((it.w & ~(kItemHeadMask | kItemNarrowBit)) != 0 || q0 >= doc_end || doc_start < 0 ||
+      q0 < doc_start || doc_end > n_tokens || h >= hq)
     return;
+  if ((it.w & kItemNarrowBit) != 0) {
+    fwd_narrow_item<E>(smem, smem_raw, q0, doc_end, doc_start, h, q, k, v, hq, hkv, o, lse,
+                       n_tokens, scale_log2);
+    return;
+  }
   const int group = hq / hkv;
   const int kvh = h / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
@@ -377,9 +636,13 @@ __global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
   lds_u16* smem = (lds_u16*)smem_raw;
 
   const int4 it = items[blockIdx.x];
-  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w;
-  if (q0 >= doc_end || doc_start < 0 || q0 < doc_start || doc_end > n_tokens || h < 0 || h >= hq)
+  const int q0 = it.x, doc_end = it.y, doc_start = it.z, h = it.w & kItemHeadMask;
+  if ((it.w & ~(kItemHeadMask | kItemNarrowBit)) != 0 || q0 >= doc_end || doc_start < 0 ||
+      q0 < doc_start || doc_end > n_tokens || h >= hq)
     return;
+  // A narrow item's 64 queries are strips 0 and 1 (strips 2 and 3 only copy and meet the
+  // barriers); q_end bounds the item's queries and keys.
+  const int q_end = min(q0 + ((it.w & kItemNarrowBit) != 0 ? BM / 2 : BM), doc_end);
   const int group = hq / hkv;
   const int kvh = h / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
@@ -388,11 +651,11 @@ __global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
   const long qrow = (long)hq * D, kvrow = (long)hkv * D;
   const int wq0 = q0 + 32 * strip;
   const int my_q = wq0 + l32;
-  const bool q_valid = my_q < doc_end;
+  const bool q_valid = my_q < q_end;
   const int ws = __builtin_amdgcn_readfirstlane(strip);
   const int wq0_u = __builtin_amdgcn_readfirstlane(wq0);
 
-  const int kv_end = min(q0 + BM, doc_end);
+  const int kv_end = q_end;
   const int n_tiles = (kv_end - doc_start + BN - 1) / BN;
 
   // Copy of tile t (K and V) into a stage: wave s moves row groups 4 s .. 4 s + 3 (4 rows each)
@@ -543,7 +806,7 @@ __global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
   // A strip past the document's end (the last item of a document whose length is not a multiple
   // of 128) has no query to compute: its wave only copies and meets the barriers, and leaves its
   // SIMD to the other work-group's wave.
-  const bool strip_live = wq0_u < doc_end;
+  const bool strip_live = wq0_u < q_end;
   auto visible = [&](int t) { return strip_live && doc_start + t * BN <= wq0_u + 31; };
   for (int t = 0; t < n_tiles; ++t) {
     const int stage = t & 1;
@@ -575,7 +838,7 @@ __global__ __launch_bounds__(fwdl::NT, 2) void fwd_lean_kernel(
                                oacc[db][8 * c + 6] * inv, oacc[db][8 * c + 7] * inv);
   static_assert(NW * 32 * (8 * 16 + 8) * 2 <= 2 * STAGE * 2, "row tiles fit in LDS");
   store_rows32<16>(smem + strip * 32 * (8 * 16 + 8), w, lane,
-                   [&](int r) { return o + (long)(wq0 + r) * qrow + h * D; }, doc_end - wq0);
+                   [&](int r) { return o + (long)(wq0 + r) * qrow + h * D; }, q_end - wq0);
   if (q_valid && hi == 0) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     __builtin_nontemporal_store((m_use + fast_log2(l_tot)) * kLn2, &lse[(long)h * n_tokens + my_q]);

@@ -45,8 +45,10 @@ constexpr int64_t kQItemCost = va::kPlanQItemCost;
 
 bool is_plan_kind(int32_t kind) {
   return kind == VA_PLAN_FWD || kind == VA_PLAN_BWD || kind == VA_PLAN_BWD_HEADS ||
-         kind == VA_PLAN_BWD_PAIRS || kind == VA_PLAN_BWD_GROUPS || kind == VA_PLAN_BWD_GROUPS_ALL;
+         kind == VA_PLAN_BWD_PAIRS || kind == VA_PLAN_BWD_GROUPS || kind == VA_PLAN_BWD_GROUPS_ALL ||
+         kind == VA_PLAN_FWD_NARROW;
 }
+bool is_fwd_kind(int32_t kind) { return kind == VA_PLAN_FWD || kind == VA_PLAN_FWD_NARROW; }
 bool is_group_kind(int32_t kind) {
   return kind == VA_PLAN_BWD_GROUPS || kind == VA_PLAN_BWD_GROUPS_ALL;
 }
@@ -60,11 +62,32 @@ int64_t doc_tiles(const int32_t* cu, int32_t n_docs) {
   return t;
 }
 
+// VA_PLAN_FWD_NARROW: the length of the documents whose last 128-query tile is split into two
+// narrow items, or 0. The split is taken when the list, split, still gives every item a CU of its
+// own: a short list (configuration 2: 192 items on 256 CUs) is as long as its longest items
+// (measured: without them the forward's span fell from 12.4 to 10.1 us), and a narrow item runs
+// their key tiles in half the chain.
+int32_t narrow_length(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t kind) {
+  if (kind != VA_PLAN_FWD_NARROW) return 0;
+  int32_t longest = 0;
+  int64_t count = 0;
+  for (int32_t i = 0; i < n_docs; ++i) {
+    const int32_t len = cu[i + 1] - cu[i];
+    if (len > longest) {
+      longest = len;
+      count = 0;
+    }
+    if (len == longest && len > 0) ++count;
+  }
+  if (longest == 0 || (doc_tiles(cu, n_docs) + count) * hq > va::kPlanCus) return 0;
+  return longest;
+}
+
 std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv,
                              int32_t kind) {
   std::vector<Item> items;
   const bool pairs =
-      kind != VA_PLAN_FWD && va::bwd_plan_pairs(doc_tiles(cu, n_docs), hq, hkv, kind);
+      !is_fwd_kind(kind) && va::bwd_plan_pairs(doc_tiles(cu, n_docs), hq, hkv, kind);
   const int32_t group = hq / hkv, rows = pairs ? (group + 1) / 2 : group;
   // Group plans: the largest group-item work that keeps the plan about as long as its VA_PLAN_BWD
   // form: that list's longest item, or its work per CU when that is more (measured at configs
@@ -83,13 +106,19 @@ std::vector<Item> make_items(const int32_t* cu, int32_t n_docs, int32_t hq, int3
       group_cap = std::max(longest, total / va::kPlanCus);
     }
   }
+  const int32_t narrow = narrow_length(cu, n_docs, hq, kind);
   for (int32_t i = 0; i < n_docs; ++i) {
     const int32_t s = cu[i], e = cu[i + 1];
     if (e <= s) continue;
-    if (kind == VA_PLAN_FWD) {
+    if (is_fwd_kind(kind)) {
       for (int32_t q0 = s; q0 < e; q0 += va::kFwdBlockM) {
         const int32_t kv_end = std::min<int64_t>((int64_t)q0 + va::kFwdBlockM, e);
         const int64_t work = kv_end - s;  // keys visited by the tile
+        if (e - s == narrow && kv_end == e) {  // the last tile of a longest document: split
+          for (int32_t q1 = q0; q1 < e; q1 += va::kFwdBlockM / 2)
+            for (int32_t h = 0; h < hq; ++h) items.push_back({q1, e, s, va::kItemNarrowBit | h, work});
+          continue;
+        }
         for (int32_t h = 0; h < hq; ++h) items.push_back({q0, e, s, h, work});
       }
     } else {
@@ -178,7 +207,8 @@ std::vector<Item> xcd_order(const std::vector<Item>& v, int32_t group) {
 }
 
 int64_t count_items(const int32_t* cu, int32_t n_docs, int32_t hq, int32_t hkv, int32_t kind) {
-  if (is_group_kind(kind)) return (int64_t)make_items(cu, n_docs, hq, hkv, kind).size();
+  if (is_group_kind(kind) || kind == VA_PLAN_FWD_NARROW)
+    return (int64_t)make_items(cu, n_docs, hq, hkv, kind).size();
   int64_t n = 0;
   const bool pairs =
       kind != VA_PLAN_FWD && va::bwd_plan_pairs(doc_tiles(cu, n_docs), hq, hkv, kind);
@@ -255,7 +285,10 @@ extern "C" int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, in
     return va::fail(VA_ESHAPE, "n_docs=%d out of range [0, %d]", n_docs, va::kPlanMaxDocs);
   if (hq <= 0 || hq > 4096) return va::fail(VA_ESHAPE, "Hq=%d out of range", hq);
   const int64_t tiles = (n_tokens + va::kFwdBlockM - 1) / va::kFwdBlockM + n_docs;
-  *capacity = tiles * hq * (kind == VA_PLAN_FWD ? 1 : 2);
+  // a narrow forward plan adds at most one item per document and head (a second half)
+  *capacity = kind == VA_PLAN_FWD ? tiles * hq
+                                  : (kind == VA_PLAN_FWD_NARROW ? (tiles + n_docs) * hq
+                                                                : tiles * hq * 2);
   return VA_OK;
 }
 
@@ -284,12 +317,12 @@ extern "C" int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_
   if (!is_plan_kind(kind)) return va::fail(VA_EINVAL, "bad plan kind %d", kind);
   if (cu_seqlens_device == nullptr) return va::fail(VA_EINVAL, "cu_seqlens_device is NULL");
   if ((rc = check_device_plan(n_tokens, n_docs, hq, hkv, kind, items_device, capacity))) return rc;
-  const bool fwd = kind == VA_PLAN_FWD;
+  const bool fwd = is_fwd_kind(kind);
   const hipError_t e = va::launch_plan_device(
       cu_seqlens_device, nullptr, n_docs, (int)n_tokens, hq, hkv, fwd ? items_device : nullptr,
       capacity, fwd ? nullptr : items_device, capacity, kind,
-      kind == VA_PLAN_BWD_GROUPS ? 1 : (kind == VA_PLAN_BWD_GROUPS_ALL ? 2 : 0), nullptr,
-      (hipStream_t)stream);
+      kind == VA_PLAN_BWD_GROUPS ? 1 : (kind == VA_PLAN_BWD_GROUPS_ALL ? 2 : 0),
+      kind == VA_PLAN_FWD_NARROW, nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return va::fail((int)e, "va_plan_build_device launch: %s", hipGetErrorString(e));
   return VA_OK;
 }
@@ -305,7 +338,7 @@ extern "C" int va_plan_build_device_lengths(const int64_t* lengths_device, int32
   if (fwd_items_device == nullptr && bwd_items_device == nullptr)
     return va::fail(VA_EINVAL, "no plan requested");
   if (fwd_items_device != nullptr &&
-      (rc = check_device_plan(n_tokens, n_docs, hq, hkv, VA_PLAN_FWD, fwd_items_device,
+      (rc = check_device_plan(n_tokens, n_docs, hq, hkv, VA_PLAN_FWD_NARROW, fwd_items_device,
                               fwd_capacity)))
     return rc;
   if (bwd_items_device != nullptr &&
@@ -314,7 +347,7 @@ extern "C" int va_plan_build_device_lengths(const int64_t* lengths_device, int32
     return rc;
   const hipError_t e = va::launch_plan_device(
       nullptr, lengths_device, n_docs, (int)n_tokens, hq, hkv, fwd_items_device, fwd_capacity,
-      bwd_items_device, bwd_capacity, VA_PLAN_BWD, 0, cu_seqlens_out, (hipStream_t)stream);
+      bwd_items_device, bwd_capacity, VA_PLAN_BWD, 0, 1, cu_seqlens_out, (hipStream_t)stream);
   if (e != hipSuccess)
     return va::fail((int)e, "va_plan_build_device_lengths launch: %s", hipGetErrorString(e));
   return VA_OK;

@@ -67,10 +67,11 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
                                                   int n_tokens, int hq, int hkv,
                                                   int4* __restrict__ fwd_items, long fwd_capacity,
                                                   int4* __restrict__ bwd_items, long bwd_capacity,
-                                                  int bwd_kind, int bwd_groups,
+                                                  int bwd_kind, int bwd_groups, int fwd_narrow,
                                                   int32_t* __restrict__ cu_out) {
   __shared__ int s_bound[kPlanMaxDocs + 1];  // clamped, non-decreasing document bounds
   __shared__ int s_tbase[kPlanMaxDocs + 1];  // exclusive prefix of the per-document tile counts
+  __shared__ int s_mbase[kPlanMaxDocs + 1];  // exclusive prefix count of the longest documents
   __shared__ int s_cnt[kBuckets];
   __shared__ long long s_scan[PT];
   const int tid = threadIdx.x;
@@ -155,22 +156,63 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
   }
   __syncthreads();
   const int n_tiles = s_tbase[n_docs];
-  const int n_cand = kind == VA_PLAN_FWD ? n_tiles : 2 * n_tiles;
+  // VA_PLAN_FWD_NARROW (plan.cpp's rule): the last tile of every document of the maximal length
+  // splits into narrow 64-query items when (T + those documents) Hq <= 256 CUs; the second
+  // halves (of last tiles over 64 queries) are the candidates n_tiles .. n_tiles + n_second - 1.
+  int narrow_len = 0, n_second = 0;
+  if (kind == VA_PLAN_FWD && fwd_narrow) {
+    long long lmax = 0;
+#pragma unroll
+    for (int i = 0; i < DPB; ++i) {
+      const int d = tid * DPB + i;
+      if (d < n_docs) lmax = max(lmax, (long long)(s_bound[d + 1] - s_bound[d]));
+    }
+    block_scan<kScanMax>(lmax, s_scan);
+    lmax = s_scan[PT - 1];
+    __syncthreads();
+    int cnt[DPB];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < DPB; ++i) {
+      const int d = tid * DPB + i;
+      cnt[i] = d < n_docs && lmax > 0 && s_bound[d + 1] - s_bound[d] == lmax;
+      sum += cnt[i];
+    }
+    const int incl = (int)block_scan<kScanSum>(sum, s_scan);
+    int run = incl - sum;
+#pragma unroll
+    for (int i = 0; i < DPB; ++i) {
+      const int d = tid * DPB + i;
+      if (d <= n_docs) s_mbase[d] = run;
+      run += cnt[i];
+    }
+    __syncthreads();
+    const int n_max = s_mbase[n_docs];
+    if (lmax > 0 && (long long)(n_tiles + n_max) * hq <= kPlanCus) {
+      narrow_len = (int)lmax;
+      n_second = narrow_len - kTile * (tiles_of(narrow_len) - 1) > kTile / 2 ? n_max : 0;
+    }
+  }
+  const int n_cand = kind == VA_PLAN_FWD ? n_tiles + n_second : 2 * n_tiles;
   // kv items of two heads each: the host planner's rule over the same tile count
   const bool pairs = kind == VA_PLAN_BWD && bwd_plan_pairs(n_tiles, hq, hkv, bwd_kind);
 
-  // Candidate c -> (document, tile, is_q): kv tiles first, then q tiles (backward).
+  // Candidate c -> (document, tile, is_q): kv tiles first, then q tiles (backward). Forward
+  // candidates past the tiles are the second narrow halves (is_q = 1 marks them there), in the
+  // order of their documents.
   auto decode = [&](int c, int& doc, int& t, int& is_q) {
     is_q = c >= n_tiles;
-    const int ct = is_q ? c - n_tiles : c;
-    int lo = 0, hi = n_docs - 1;  // last document with tbase <= ct (it has tiles)
+    const bool second = kind == VA_PLAN_FWD && is_q;
+    const int ct = second ? c - n_tiles : (is_q ? c - n_tiles : c);
+    const int* base = second ? s_mbase : s_tbase;
+    int lo = 0, hi = n_docs - 1;  // last document with base <= ct
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (s_tbase[mid] <= ct) lo = mid;
+      if (base[mid] <= ct) lo = mid;
       else hi = mid - 1;
     }
     doc = lo;
-    t = ct - s_tbase[lo];
+    t = second ? tiles_of(s_bound[lo + 1] - s_bound[lo]) - 1 : ct - s_tbase[lo];
   };
   // The host planner's work measures (plan.cpp): of a per-head item (w1) and of a pair item (w2)
   // of the candidate; `steps` the query steps of a kv candidate (0 for the others).
@@ -273,13 +315,20 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
     const long pos = atomicAdd(&s_cnt[bucket(doc, t, is_q)], 1);
     const int s = s_bound[doc], e = s_bound[doc + 1];
     const int sub = group_heads(doc, t, is_q);
+    // a forward candidate's narrow items: the last tile of a longest document (is_q: its second
+    // half, 64 queries on)
+    const bool narrow = kind == VA_PLAN_FWD && narrow_len > 0 && e - s == narrow_len &&
+                        t == tiles_of(narrow_len) - 1;
+    const int q_first = s + t * kTile + (kind == VA_PLAN_FWD && is_q ? kTile / 2 : 0);
+    const int fwd_bits = narrow ? kItemNarrowBit : 0;
     for (int g = 0; g < hkv; ++g) {
       const long combo = pos * hkv + g;
       const long blk = combo / kXcds, col = combo % kXcds;
       const long ncols = min((long)kXcds, n_combos - blk * kXcds);
       for (int r = 0; r < group; ++r) {
         const long slot = blk * kXcds * group + r * ncols + col;
-        int4 item = int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
+        int4 item = kind == VA_PLAN_FWD ? int4{q_first, e, s, fwd_bits | (g * group + r)}
+                                        : int4{s + t * kTile, e, s, (is_q << 24) | (g * group + r)};
         if (sub > 0) {
           item = r < group / sub
                      ? int4{s + t * kTile, e, s,
@@ -304,10 +353,10 @@ __global__ __launch_bounds__(PT) void plan_kernel(const int32_t* __restrict__ cu
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
                               int32_t* bwd_items, long bwd_capacity, int bwd_kind,
-                              int bwd_groups, int32_t* cu_out, hipStream_t stream) {
+                              int bwd_groups, int fwd_narrow, int32_t* cu_out, hipStream_t stream) {
   hipLaunchKernelGGL(plan_kernel, dim3(2), dim3(PT), 0, stream, cu, lengths, n_docs, n_tokens, hq,
                      hkv, (int4*)fwd_items, fwd_capacity, (int4*)bwd_items, bwd_capacity,
-                     bwd_kind, bwd_groups, cu_out);
+                     bwd_kind, bwd_groups, fwd_narrow, cu_out);
   return hipGetLastError();
 }
 

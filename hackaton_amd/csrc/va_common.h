@@ -250,7 +250,7 @@ struct SameColumn {
 template <int C, class RowPtr, class ColMap = SameColumn>
 __device__ inline void store_rows32(lds_u16* tile, const u32x4 (&w)[C / 2], int lane,
                                     RowPtr row_ptr, int n_rows, ColMap col_map = ColMap{}) {
-  static_assert(C == 8 || C == 16, "64 or 128 columns");
+  static_assert(C == 4 || C == 8 || C == 16, "32, 64 or 128 columns");
   constexpr int LT = 8 * C + 8;
   const int l32 = lane & 31, hi = lane >> 5;
 #pragma unroll

@@ -38,6 +38,10 @@ constexpr int kItemHeadsShift = 12;
 // Hkv width (the tile needs no per-head partials and no GQA sum); with S < G it writes the sum of
 // its S heads into the partial of head h, and the GQA sum adds G / S partials for the tile's rows.
 constexpr int kItemGroupBit = 1 << 21;
+// A narrow forward item (VA_PLAN_FWD_NARROW): 64 queries instead of 128, run by the 8-wave
+// forward as 2 query strips x 4 key phases, so that its chain of key tiles is half a 128-query
+// item's. The host plan splits its longest items so when the list leaves CUs idle.
+constexpr int kItemNarrowBit = 1 << 22;
 // Planners' work measure of a group item over S heads of a kv tile with `steps` query steps: the
 // halves take ceil(S steps / 2) step pairs.
 __host__ __device__ inline int64_t bwd_group_work(int64_t steps, int s) {
@@ -158,7 +162,7 @@ hipError_t launch_pack_rows(const void* src, void* dst, const int32_t* b_idx, co
 hipError_t launch_plan_device(const int32_t* cu, const int64_t* lengths, int n_docs, int n_tokens,
                               int hq, int hkv, int32_t* fwd_items, long fwd_capacity,
                               int32_t* bwd_items, long bwd_capacity, int bwd_kind,
-                              int bwd_groups,
+                              int bwd_groups, int fwd_narrow,
                               int32_t* cu_out, hipStream_t stream);
 
 }  // namespace va

@@ -52,7 +52,7 @@ enum {
 
 enum { VA_F16 = 0, VA_BF16 = 1, VA_F32 = 2 };
 enum { VA_PLAN_FWD = 0, VA_PLAN_BWD = 1, VA_PLAN_BWD_HEADS = 2, VA_PLAN_BWD_PAIRS = 3,
-       VA_PLAN_BWD_GROUPS = 4, VA_PLAN_BWD_GROUPS_ALL = 5 };
+       VA_PLAN_BWD_GROUPS = 4, VA_PLAN_BWD_GROUPS_ALL = 5, VA_PLAN_FWD_NARROW = 6 };
 enum { VA_BWD_PAIR_MIN_ITEMS = 1024 };
 enum { VA_LAYOUT_PACKED = 0, VA_LAYOUT_PADDED = 1 };
 enum { VA_BWD_MAIN = 1, VA_BWD_FINISH = 2, VA_BWD_FINISH_HEADS = 3, VA_BWD_STATS = 4,
@@ -78,7 +78,12 @@ int32_t va_head_dim(void);
  * list, or than that list's work per CU (256 CUs); S < G only in lists with pair items). An item
  * of S = G heads writes the tile's dK/dV itself (Hkv width): no per-head partials, nothing for
  * the GQA sum; one of S < G heads writes the sum of its heads into the first head's partial.
- * Item word: kind << 24 | group << 21 | pair << 20 | (S - 1) << 12 | head.
+ * Item word: kind << 24 | narrow << 22 | group << 21 | pair << 20 | (S - 1) << 12 | head.
+ * VA_PLAN_FWD_NARROW (host plans only) is VA_PLAN_FWD whose longest items are split in two
+ * 64-query items (narrow bit 22) when the list is short enough to leave CUs idle: for the
+ * last 128-query tile of every document of the maximal length L, when (T + the number of such
+ * documents) x Hq <= 256 (T as below). Both forward kernels run narrow items; the 8-wave one
+ * walks a narrow item's keys in four phases, so that its chain of key tiles is half as long.
  * VA_PLAN_BWD_GROUPS_ALL gives every key tile S = G. Group plans need Hq > Hkv; with dk = dv =
  * NULL their per-head partials hold each group item's sum in its first head (see va_bwd). Every
  * plan kind gives the same outputs up to rounding

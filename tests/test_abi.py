@@ -59,6 +59,57 @@ def test_forward_plan_covers_every_query_tile_once(lengths, hq, hkv):
     check_xcd_order(items, hq, hkv, lambda q0, e, s, w: min(q0 + 128, e) - s)
 
 
+NARROW = 1 << 22  # item word bit of a narrow (64-query) forward item
+
+
+@pytest.mark.parametrize("lengths", [[512] * 4, [64, 37, 50, 12], [1, 1, 1], [129, 0, 300],
+                                     [4096, 17], [450, 450, 60], [100, 450]])
+@pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (12, 12)])
+def test_narrow_forward_plan_splits_the_longest_items_of_short_lists(lengths, hq, hkv):
+    """VA_PLAN_FWD_NARROW: when (T + the number of longest documents) x Hq <= 256 (T = the sum of
+    ceil(length / 128)), the last 128-query tile of every document of the maximal length becomes
+    narrow items of 64 queries (the second only where the tile has more than 64 queries), and
+    every (query, head) is still covered once; otherwise the list is VA_PLAN_FWD's."""
+    cu, plain = plan(lengths, hq, hkv, _lib.VA_PLAN_FWD)
+    _, items = plan(lengths, hq, hkv, _lib.VA_PLAN_FWD_NARROW)
+    longest = max(lengths)
+    tiles = sum(-(-x // 128) for x in lengths if x > 0)
+    split = (tiles + lengths.count(longest)) * hq <= 256
+    covered = set()
+    for q0, e, s, w in items.tolist():
+        h = w & ~NARROW
+        assert 0 <= h < hq and w & ~(NARROW | 0xFFF) == 0
+        n = 64 if w & NARROW else 128
+        if w & NARROW:
+            assert split and e - s == longest and e - q0 <= 128 and (q0 - s) % 64 == 0
+        else:
+            assert (q0 - s) % 128 == 0 and not (split and e - s == longest and q0 + 128 >= e)
+        covered.update((q, h) for q in range(q0, min(q0 + n, e)))
+    assert len(covered) == sum(lengths) * hq
+    assert sum(min(q0 + (64 if w & NARROW else 128), e) - q0 for q0, e, s, w in
+               items.tolist()) == sum(lengths) * hq  # no query twice
+    if not split:
+        assert items.tolist() == plain.tolist()
+    else:
+        assert len(items) <= 256
+        # the planner's work measure of a narrow item is its whole tile's (both halves alike)
+        check_xcd_order(items, hq, hkv,
+                        lambda q0, e, s, w: (e if w & NARROW else min(q0 + 128, e)) - s)
+    cap = ctypes.c_int64()
+    assert _lib.lib().va_plan_capacity(sum(lengths), len(lengths), hq, _lib.VA_PLAN_FWD_NARROW,
+                                       ctypes.byref(cap)) == _lib.VA_OK
+    assert len(items) <= cap.value == (-(-sum(lengths) // 128) + 2 * len(lengths)) * hq
+
+
+def test_configuration_2_forward_list_splits_its_48_longest_items():
+    """At configuration 2 (4 x 512 tokens, 12 heads) the 48 items over 512 keys become 96 narrow
+    items: 240 items for 256 CUs."""
+    _, items = plan([512] * 4, 12, 2, _lib.VA_PLAN_FWD_NARROW)
+    narrow = items[(items[:, 3] & NARROW) != 0]
+    assert len(items) == 240 and len(narrow) == 96
+    assert sorted(set((narrow[:, 0] - narrow[:, 2]).tolist())) == [384, 448]
+
+
 HEAD_MASK = (1 << 12) - 1  # item word: kind << 24 | group << 21 | pair << 20 | (S-1) << 12 | head
 
 

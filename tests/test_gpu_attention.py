@@ -129,6 +129,48 @@ def test_many_item_forward_matches_oracle(lengths, hq, hkv, dtype):
     check_all(out.cpu(), (dq.cpu(), dk.cpu(), dv.cpu()), ref, dtype, n, hq)
 
 
+@pytest.mark.parametrize("lengths,hq,hkv,dtype", [([512] * 4, 12, 2, torch.float16),
+                                                   ([450, 450, 60], 12, 2, torch.bfloat16),
+                                                   ([200, 70, 33], 28, 4, torch.bfloat16)])
+def test_narrow_forward_items_match_the_oracle(lengths, hq, hkv, dtype):
+    """The host plan splits the last tile of the longest documents into narrow 64-query items
+    (VA_PLAN_FWD_NARROW: configuration 2's 48 longest items, partial second halves of 450-token
+    documents, G = 7): O and lse of both forward kernels over that list (the 8-wave kernel's
+    four-phase walk, the many-item kernel over the list padded with empty items) against the
+    oracle, and against the same kernel over the unsplit list to rounding."""
+    banner("narrow forward", lengths, hq, hkv, dtype)
+    q, k, v, do = wl.make_inputs(lengths, hq, hkv, dtype, seed=sum(lengths) + hq)
+    n = sum(lengths)
+    dev = torch.device("cuda")
+    plan = att._plan(att._cu_seqlens(lengths, dev), hq, hkv)
+    narrow = (plan.fwd_items[: plan.n_fwd, 3] & (1 << 22)) != 0
+    assert bool(narrow.any())
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    plain = torch.from_numpy(att.build_plan_host(cu, hq, hkv, att._lib.VA_PLAN_FWD)).to(dev)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    code = 0 if dtype == torch.float16 else 1
+    ref = oracle(q, k, v, do, lengths)
+
+    def run(kernel, items):
+        out = torch.full_like(qd, float("nan"))
+        lse = torch.full((hq, n), float("nan"), dtype=torch.float32, device=dev)
+        att.check(att.lib().va_fwd_kernel(kernel, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                          out.data_ptr(), lse.data_ptr(), items.data_ptr(),
+                                          items.shape[0], n, hq, hkv, 128, SCALE, code,
+                                          att._stream()), "va_fwd_kernel")
+        torch.cuda.synchronize()
+        return out, lse
+    for kernel, items, unsplit in ((att._lib.VA_FWD_WIDE, plan.fwd_items[: plan.n_fwd], plain),
+                                   (att._lib.VA_FWD_MANY, padded_fwd_plan(plan, 512), plain)):
+        out, lse = run(kernel, items)
+        err_o = float(np.max(np.abs(out.cpu().float().numpy().reshape(n, hq, 128) - ref[0])))
+        err_lse = float(np.max(np.abs(lse.cpu().numpy() - ref[1])))
+        assert err_o <= TOL[dtype]["o"] and err_lse <= TOL[dtype]["lse"], (kernel, err_o, err_lse)
+        out2, lse2 = run(kernel, unsplit)
+        assert float((out.float() - out2.float()).abs().max()) <= TOL[dtype]["o"], kernel
+        assert float((lse - lse2).abs().max()) <= TOL[dtype]["lse"], kernel
+
+
 class _Plan:
     """A plan object for attention_forward / attention_backward from explicit item lists."""
 
@@ -578,7 +620,7 @@ def plan_work(kind, a, e, s, w):
     """The planners' work measure of an item: keys visited (forward); MFMAs per wave per
     iteration plus the item's fixed cost (backward; a pair item's halves take every step, a
     group item's the steps of its S heads)."""
-    if kind == 0:
+    if kind in (0, 6):  # VA_PLAN_FWD, VA_PLAN_FWD_NARROW (a narrow item: its whole tile's)
         return min(a + 128, e) - s
     if w >> 24 == 0:
         steps = (e - a + 31) // 32
@@ -636,7 +678,8 @@ def test_device_plan_matches_host_plan(lengths):
     tiles = sum(-(-x // 128) for x in lengths if x > 0)
     pairs = 2 * tiles * hq >= att._lib.VA_BWD_PAIR_MIN_ITEMS
     part_items, part_n = dplan.partial_bwd()
-    for kind, items, count in ((0, dplan.fwd_items, dplan.n_fwd), (1, part_items, part_n),
+    narrow = att._lib.VA_PLAN_FWD_NARROW
+    for kind, items, count in ((narrow, dplan.fwd_items, dplan.n_fwd), (1, part_items, part_n),
                                (groups, dplan.bwd_items, dplan.n_bwd)):
         host = att.build_plan_host(cu, hq, hkv, kind)
         got = items.cpu().numpy()[:count]
