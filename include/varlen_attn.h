@@ -79,7 +79,7 @@ int32_t va_head_dim(void);
  * of S = G heads writes the tile's dK/dV itself (Hkv width): no per-head partials, nothing for
  * the GQA sum; one of S < G heads writes the sum of its heads into the first head's partial.
  * Item word: kind << 24 | narrow << 22 | group << 21 | pair << 20 | (S - 1) << 12 | head.
- * VA_PLAN_FWD_NARROW (host plans only) is VA_PLAN_FWD whose longest items are split in two
+ * VA_PLAN_FWD_NARROW is VA_PLAN_FWD whose longest items are split in two
  * 64-query items (narrow bit 22) when the list is short enough to leave CUs idle: for the
  * last 128-query tile of every document of the maximal length L, when (T + the number of such
  * documents) x Hq <= 256 (T as below). Both forward kernels run narrow items; the 8-wave one
@@ -110,8 +110,9 @@ int va_plan_bwd_row_stats(const int32_t* cu_seqlens, int32_t n_docs, int32_t* us
  * by one kernel on `stream`, with no host read (the reference reads the lengths back with
  * lengths.tolist(), solution/packed.py:170-172, before _cu_seqlens at attention.py:195-209).
  * va_plan_capacity gives, from host-known sizes only, the number of items such a plan has:
- * ceil(n_tokens / 128) + n_docs tiles per query head, twice that for the backward kinds (a pair
- * plan leaves the slots of its missing kv rows empty).
+ * ceil(n_tokens / 128) + n_docs tiles per query head (+ n_docs for VA_PLAN_FWD_NARROW's second
+ * halves), twice that for the backward kinds (a pair plan leaves the slots of its missing kv rows
+ * empty).
  * va_plan_build_device writes exactly `capacity` items (int32 x 4) to device memory: the real
  * ones longest first, then empty items that va_fwd / va_bwd skip, so the kernels take n_items =
  * capacity. Document bounds are clamped into [0, n_tokens] and made non-decreasing on the device,
@@ -125,7 +126,8 @@ int va_plan_build_device(const int32_t* cu_seqlens_device, int32_t n_docs, int64
 
 /* The same plans straight from the per-document lengths (int64, as a mask's row sums give them):
  * one launch builds cu_seqlens (into cu_seqlens_out, n_docs + 1 int32, when it is non-NULL), the
- * forward plan and the backward plan (either item pointer may be NULL to skip that kind). Each
+ * forward plan (kind VA_PLAN_FWD_NARROW, capacity from va_plan_capacity of that kind) and the
+ * backward plan (VA_PLAN_BWD; either item pointer may be NULL to skip that kind). Each
  * length is clamped into [0, n_tokens] and the bounds saturate at n_tokens.
  * Replaces: lengths.tolist() at solution/packed.py:170-172 and _cu_seqlens at
  * solution/attention.py:195-209, on the device. */
