@@ -285,10 +285,12 @@ extern "C" int va_plan_capacity(int64_t n_tokens, int32_t n_docs, int32_t hq, in
     return va::fail(VA_ESHAPE, "n_docs=%d out of range [0, %d]", n_docs, va::kPlanMaxDocs);
   if (hq <= 0 || hq > 4096) return va::fail(VA_ESHAPE, "Hq=%d out of range", hq);
   const int64_t tiles = (n_tokens + va::kFwdBlockM - 1) / va::kFwdBlockM + n_docs;
-  // a narrow forward plan adds at most one item per document and head (a second half)
+  // A narrow forward plan adds at most one item per document and head (a second half), and only
+  // to a list that then holds at most kPlanCus items.
   *capacity = kind == VA_PLAN_FWD ? tiles * hq
-                                  : (kind == VA_PLAN_FWD_NARROW ? (tiles + n_docs) * hq
-                                                                : tiles * hq * 2);
+              : kind == VA_PLAN_FWD_NARROW
+                  ? std::max<int64_t>(tiles * hq, std::min<int64_t>(va::kPlanCus, (tiles + n_docs) * hq))
+                  : tiles * hq * 2;
   return VA_OK;
 }
 

@@ -110,9 +110,9 @@ int va_plan_bwd_row_stats(const int32_t* cu_seqlens, int32_t n_docs, int32_t* us
  * by one kernel on `stream`, with no host read (the reference reads the lengths back with
  * lengths.tolist(), solution/packed.py:170-172, before _cu_seqlens at attention.py:195-209).
  * va_plan_capacity gives, from host-known sizes only, the number of items such a plan has:
- * ceil(n_tokens / 128) + n_docs tiles per query head (+ n_docs for VA_PLAN_FWD_NARROW's second
- * halves), twice that for the backward kinds (a pair plan leaves the slots of its missing kv rows
- * empty).
+ * ceil(n_tokens / 128) + n_docs tiles per query head (VA_PLAN_FWD_NARROW: n_docs more, its
+ * second halves, up to 256 items in all), twice that for the backward kinds (a pair plan leaves
+ * the slots of its missing kv rows empty).
  * va_plan_build_device writes exactly `capacity` items (int32 x 4) to device memory: the real
  * ones longest first, then empty items that va_fwd / va_bwd skip, so the kernels take n_items =
  * capacity. Document bounds are clamped into [0, n_tokens] and made non-decreasing on the device,
