@@ -7,7 +7,10 @@ raises, so nothing can silently run another attention implementation.
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libvarlen_attn.so")
+# VA_LIB_PATH names another build of the same library (the host-sanitized one of
+# hackaton_amd.build_hostsan, for the CPU tests); by default the in-tree build.
+LIB_PATH = os.environ.get("VA_LIB_PATH") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libvarlen_attn.so")
 
 VA_OK, VA_EINVAL, VA_ESHAPE, VA_EDTYPE, VA_ESEQ, VA_ECAPACITY = 0, -1, -2, -3, -4, -5
 VA_F16, VA_BF16, VA_F32 = 0, 1, 2
