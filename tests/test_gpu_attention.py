@@ -545,12 +545,19 @@ def test_packed_attention_matches_oracle(name, lengths, heads, kv_heads, dtype):
         assert q_shapes == {0} and kv_shapes == {0} and not plan.bwd_finish
     else:  # every kv shape, the row statistics pass
         assert kv_shapes == {0, 1, 2} and plan.bwd_stats
+    check_packed_attention(lengths, heads, kv_heads, dtype)
+
+
+def check_packed_attention(lengths, heads, kv_heads, dtype, seed=1):
+    """packed_attention forward and backward on random projections of the packed rows of
+    `lengths` (right-padded batch, rotary tables of test length) against the oracle's fp32
+    rotation, fp64 attention and fp32 inverse rotation."""
     seq = max(lengths)
     rows = torch.tensor([b * seq + t for b, length in enumerate(lengths) for t in range(length)])
     b_idx, t_idx = (rows // seq).to(torch.int32), (rows % seq).to(torch.int32)
     n = rows.numel()
     cos, sin = rope_tables(seq)
-    g = torch.Generator().manual_seed(1)
+    g = torch.Generator().manual_seed(seed)
     q = (torch.randn(n, heads * 128, generator=g) * 0.5).to(dtype)
     k = (torch.randn(n, kv_heads * 128, generator=g) * 0.5).to(dtype)
     v = torch.randn(n, kv_heads * 128, generator=g).to(dtype)

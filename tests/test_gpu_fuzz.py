@@ -15,7 +15,8 @@ import torch
 
 from hackaton_amd import attention as att
 from hackaton_amd import workloads as wl
-from tests.test_gpu_attention import SCALE, banner, check_all, oracle, run_varlen
+from tests.test_gpu_attention import (SCALE, banner, check_all, check_packed_attention, oracle,
+                                      run_varlen)
 
 pytestmark = pytest.mark.gpu
 
@@ -69,3 +70,29 @@ def test_random_batches_match_oracle_device_lengths_and_rerun(i, lengths, hq, hk
     torch.cuda.synchronize()
     for a, b in zip(host, (out.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu())):
         assert torch.equal(a, b), "device lengths differ from host lengths"
+
+
+def packed_fuzz_cases(n=12, seed=20261203):
+    """Batches for the installed path: short lists (the per-head partials and the inverse rotation
+    pass) and, every third case, lists long enough for the rotary epilogues (ceil(N / 128) Hq >=
+    512)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        hq, hkv = SHAPES[(i + 1) % len(SHAPES)]
+        dtype = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+        long_batch = i % 3 == 2
+        target = (512 // hq + 2) * 128 if long_batch else int(rng.integers(50, 1200))
+        lengths = []
+        while sum(lengths) < target:
+            lengths.append(int(rng.choice(EDGES)) if rng.random() < 0.3
+                           else int(rng.integers(1, 700)))
+        cases.append((i, lengths, hq, hkv, dtype))
+    return cases
+
+
+@pytest.mark.parametrize("i,lengths,hq,hkv,dtype", packed_fuzz_cases())
+def test_random_batches_through_packed_attention_match_oracle(i, lengths, hq, hkv, dtype):
+    banner("packed fuzz", i, len(lengths), sum(lengths), hq, hkv, dtype,
+           "rotary epilogues" if att.rotary_epilogues(sum(lengths), hq) else "partials route")
+    check_packed_attention(lengths, hq, hkv, dtype, seed=2000 + i)
