@@ -211,6 +211,56 @@ def time_cpu(fn, args, warmup=2, reps=5, budget_s=2.5):
     return best
 
 
+def measure_ceilings(reps=5):
+    """The two ceilings the roofline fractions are quoted against, measured on this box with the
+    library's probes (va_probe_mfma, va_probe_copy): dense 32x32x16 MFMA issue rate in fp16 and
+    bf16 (2048 work-groups of 4 waves, 4 independent accumulators per wave) and the streaming rate
+    of a 1 GiB device copy (read + written bytes), each the median of `reps` launches timed with
+    HIP events on the launch stream."""
+    import torch
+
+    from hackaton_amd import _lib
+
+    lib = _lib.lib()
+    st = torch.cuda.current_stream()
+    blocks, iters = 2048, 2000
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    flops = blocks * 4 * iters * 4 * 32 * 32 * 16 * 2
+
+    def timed(launch):
+        launch()
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(st)
+            launch()
+            b.record(st)
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        return sorted(times)[len(times) // 2]
+
+    out = {}
+    for name, code in (("mfma_f16_tflops", _lib.VA_F16), ("mfma_bf16_tflops", _lib.VA_BF16)):
+        ms = timed(lambda: _lib.check(lib.va_probe_mfma(code, blocks, iters, sink.data_ptr(),
+                                                        st.cuda_stream), "va_probe_mfma"))
+        out[name] = round(flops / (ms * 1e-3) / 1e12, 1)
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    # one round of 4 chunks per thread (65536 work-groups: the best of 1024-65536 on the box)
+    ms = timed(lambda: _lib.check(lib.va_probe_copy(src.data_ptr(), dst.data_ptr(), n, 65536,
+                                                    st.cuda_stream), "va_probe_copy"))
+    out["hbm_copy_gbs"] = round(2 * n / (ms * 1e-3) / 1e9, 1)
+    out["datasheet"] = {"mfma_tflops": PEAK_MFMA_TFLOPS["float16"], "hbm_gbs": PEAK_HBM_GBS}
+    out["method"] = ("va_probe_mfma: 2048 work-groups x 4 waves x 2000 rounds of 4 independent "
+                     "v_mfma_f32_32x32x16; va_probe_copy: 1 GiB (4x the 256 MB last-level "
+                     "cache), 65536 work-groups, 16 B per lane, read + write bytes; median of 5 "
+                     "launches")
+    del src, dst, sink
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(configs=(1, 2)):
     """The reference's CPU-runnable math on this host's cores (fp32, forward + backward), both
     constructions, at each configuration's shape; the faster construction of the last
@@ -618,6 +668,9 @@ def main(argv=None):
             installed[f"config{cfg_i}"] = r
             print(f"[bench] installed path config {cfg_i}: {json.dumps(r)}", flush=True)
 
+    ceilings = measure_ceilings()
+    print(f"[bench] measured ceilings {json.dumps(ceilings)}", flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline((1, args.config))
@@ -646,6 +699,7 @@ def main(argv=None):
         "kernels_tflops": {k: round(models[k]["flops"] / (v * 1e-6) / 1e12, 2)
                            for k, v in kus.items() if models[k]["flops"]},
         "roofline": roofline_,
+        "ceilings_measured": ceilings,
         "by_config": by_config,
         "installed_path": installed,
         "cpu_baseline": cpu,

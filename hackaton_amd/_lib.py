@@ -70,6 +70,8 @@ SIGNATURES = {
     "va_rope_bwd": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i32,
                                    _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "va_pack_rows": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p]),
+    "va_probe_mfma": (ctypes.c_int, [_i32, _i32, _i32, _p, _p]),
+    "va_probe_copy": (ctypes.c_int, [_p, _p, _i64, _i32, _p]),
 }
 
 _LIB = None

@@ -14,8 +14,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libvarlen_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
-SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "rope.hip", "plan_device.hip", "noalloc.hip", "api.cpp",
-           "plan.cpp"]
+SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "rope.hip", "plan_device.hip", "noalloc.hip", "probe.hip",
+           "api.cpp", "plan.cpp"]
 ARCH = os.environ.get("VA_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops off: no packed fp32 VALU instructions are generated.

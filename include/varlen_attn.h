@@ -272,6 +272,17 @@ int va_pack_rows(const void* src, void* dst, const int32_t* b_idx, const int32_t
                  int64_t n_tokens, int32_t heads, int32_t seq, int32_t head_dim,
                  int32_t elem_bytes, int32_t mode, void* stream);
 
+/* ---- machine-ceiling probes (diagnostics) ----------------------------------------------------
+ * No counterpart in the reference: the benchmark measures with them the two ceilings it quotes
+ * its roofline fractions against, on the box it runs on, beside the data-sheet figures.
+ * va_probe_mfma: `blocks` work-groups of 256 threads, each wave issuing `iters` rounds of 4
+ * independent v_mfma_f32_32x32x16 (VA_F16 or VA_BF16) MFMAs, i.e. blocks * 4 * iters * 4 * 32768
+ * FLOPs; `sink` (blocks * 256 floats) receives one value per thread. va_probe_copy: dst = src over
+ * `bytes` (a multiple of 16, both 16-byte aligned), 16 bytes per lane, `blocks` work-groups of
+ * 256 threads striding over the buffer. */
+int va_probe_mfma(int32_t dtype, int32_t blocks, int32_t iters, float* sink, void* stream);
+int va_probe_copy(const void* src, void* dst, int64_t bytes, int32_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -453,6 +453,22 @@ def test_noalloc_refuses_sizes_beyond_its_scratch():
     assert limit >= 8192 * 12  # configurations 2 and 3 fit
 
 
+def test_ceiling_probes_check_arguments_before_any_launch():
+    """va_probe_mfma / va_probe_copy refuse bad arguments on the host (the fake pointers are never
+    dereferenced, nothing is launched)."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.va_probe_mfma(_lib.VA_F32, 1, 1, fake, None) == _lib.VA_EDTYPE
+    assert lib.va_probe_mfma(_lib.VA_F16, 0, 1, fake, None) == _lib.VA_EINVAL
+    assert lib.va_probe_mfma(_lib.VA_F16, 1, 0, fake, None) == _lib.VA_EINVAL
+    assert lib.va_probe_mfma(_lib.VA_BF16, 1, 1, None, None) == _lib.VA_EINVAL
+    assert lib.va_probe_copy(None, fake, 16, 1, None) == _lib.VA_EINVAL
+    assert lib.va_probe_copy(fake, fake, 24, 1, None) == _lib.VA_EINVAL
+    assert lib.va_probe_copy(fake, fake, 16, 0, None) == _lib.VA_EINVAL
+    assert lib.va_probe_copy(ctypes.c_void_p(0x1008), fake, 16, 1, None) == _lib.VA_EINVAL
+    assert lib.va_probe_copy(fake, fake, 0, 1, None) == _lib.VA_OK  # nothing to copy
+
+
 def test_row_statistics_rule():
     """va_plan_bwd_row_stats: the mean over query rows of the 128-key tiles at or before the
     row's own, against VA_BWD_STATS_MIN_TILES = 3. Closed forms: a document of 128 m rows covers

@@ -1220,3 +1220,24 @@ def test_rope_forward_passes_v_through_when_it_needs_no_cast():
     assert torch.equal(va, vb) and torch.equal(vb.reshape(n, -1), v)
     with pytest.raises(ValueError, match="share a dtype"):
         att.rope_forward(q, k, v.float(), cos, sin, b_idx, t_idx, heads, kv_heads, torch.float16)
+
+
+def test_ceiling_probes_run_and_copy_exactly():
+    """The benchmark's ceiling probes: va_probe_mfma runs in fp16 and bf16 and leaves a finite
+    value per thread; va_probe_copy copies a buffer (with a ragged tail past its last full
+    stride) exactly."""
+    banner("ceiling probes")
+    lib = att._lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    sink = torch.full((8 * 256,), float("nan"), device="cuda")
+    for code in (att._lib.VA_F16, att._lib.VA_BF16):
+        att._lib.check(lib.va_probe_mfma(code, 8, 10, sink.data_ptr(), stream), "va_probe_mfma")
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(sink).all())
+    n = 3 * 256 * 16 * 4 * 16 + 48  # bytes: three grid strides of 4 chunks and a short tail
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.zeros_like(src)
+    att._lib.check(lib.va_probe_copy(src.data_ptr(), dst.data_ptr(), n, 16, stream),
+                   "va_probe_copy")
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
