@@ -214,7 +214,7 @@ def time_cpu(fn, args, warmup=2, reps=5, budget_s=2.5):
 def measure_ceilings(reps=5):
     """The two ceilings the roofline fractions are quoted against, measured on this box with the
     library's probes (va_probe_mfma, va_probe_copy): dense 32x32x16 MFMA issue rate in fp16 and
-    bf16 (2048 work-groups of 4 waves, 4 independent accumulators per wave) and the streaming rate
+    bf16 (4096 work-groups of 4 waves, 4 independent accumulators per wave) and the streaming rate
     of a 1 GiB device copy (read + written bytes), each the median of `reps` launches timed with
     HIP events on the launch stream."""
     import torch
@@ -223,7 +223,8 @@ def measure_ceilings(reps=5):
 
     lib = _lib.lib()
     st = torch.cuda.current_stream()
-    blocks, iters = 2048, 2000
+    # 16 waves per SIMD over the kernel, ~4 ms per launch: the launch's own cost is under 1%
+    blocks, iters = 4096, 4000
     sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
     flops = blocks * 4 * iters * 4 * 32 * 32 * 16 * 2
 
@@ -252,7 +253,7 @@ def measure_ceilings(reps=5):
                                                     st.cuda_stream), "va_probe_copy"))
     out["hbm_copy_gbs"] = round(2 * n / (ms * 1e-3) / 1e9, 1)
     out["datasheet"] = {"mfma_tflops": PEAK_MFMA_TFLOPS["float16"], "hbm_gbs": PEAK_HBM_GBS}
-    out["method"] = ("va_probe_mfma: 2048 work-groups x 4 waves x 2000 rounds of 4 independent "
+    out["method"] = ("va_probe_mfma: 4096 work-groups x 4 waves x 4000 rounds of 4 independent "
                      "v_mfma_f32_32x32x16; va_probe_copy: 1 GiB (4x the 256 MB last-level "
                      "cache), 65536 work-groups, 16 B per lane, read + write bytes; median of 5 "
                      "launches")
